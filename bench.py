@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Decode-step sampler benchmark on one MI355X.
+
+Measures the sampler on the heterogeneous batch workload (B=64 rows of V=248320
+bf16 logits, per-row temperature / top-k / top-p, 10% greedy rows): sampled
+rows/s, µs per step and algorithmic HBM GB/s as a fraction of the 8 TB/s HBM
+roofline.  It also reports µs per step at B=1 (the top-k/top-p/repetition
+workload) and, on rank 0, the torch-CPU restatement of the reference sampler
+timed on the host cores over a bounded sample of the same workload.
+
+A step is one ``qs_sample`` call over one batch.  Inputs are resident in HBM
+before the timed region: the logits are held in several copies that the steps
+rotate through, so that each step reads its batch from HBM rather than from
+the 256 MB last-level cache.  Steps are captured in a HIP graph (the way the
+decode loop runs) and the graph is replayed; the timed region is bracketed by
+``torch.cuda.synchronize()`` and measured with HIP events on the stream the
+kernels run on.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+WORKLOAD = "hetero_b64_bf16"
+B1_WORKLOAD = "topk_topp_rep_bf16"
+ROTATE_BYTES = 640 << 20  # rotate through >= 640 MB of logits copies (LLC is 256 MB)
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Case:
+    """One workload staged on the device with R rotating copies of its inputs."""
+
+    def __init__(self, name: str, device, rotate_bytes: int = ROTATE_BYTES, max_copies: int = 64):
+        import numpy as np
+        import torch
+
+        from qedge_amd import workloads as W
+        from qedge_amd.sampler import Workspace
+
+        self.w = w = W.make(name)
+        self.name = name
+        B, V = w.nrows, w.V
+        self.B, self.V = B, V
+        if w.dtype == "f32":
+            base = torch.from_numpy(np.ascontiguousarray(w.logits)).to(device)
+        else:
+            base = torch.from_numpy(np.ascontiguousarray(w.logits).view(np.int16)).to(device).view(torch.bfloat16)
+        nbytes = base.numel() * base.element_size()
+        self.R = R = max(1, min(max_copies, math.ceil(rotate_bytes / nbytes)))
+        self.logits = [base] + [base.clone() for _ in range(R - 1)]
+        t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)
+        self.params = dict(temperatures=t(w.temperature, torch.float32), top_ps=t(w.top_p, torch.float32),
+                           top_ks=t(w.top_k, torch.int32), repetition_penalties=t(w.rep, torch.float32),
+                           presence_penalties=t(w.pres, torch.float32),
+                           frequency_penalties=t(w.freq, torch.float32), history=t(w.history, torch.int32))
+        self.uniforms = [t(w.uniforms(s), torch.float32) for s in range(R)]
+        H = 0 if w.history is None else w.history.shape[1]
+        self.ws = Workspace(B, V, base.dtype, H, device)
+        self.ids = torch.empty(B, dtype=torch.int64, device=device)
+        self.alg_bytes = w.algorithmic_bytes()
+
+    def step(self, i: int) -> None:
+        from qedge_amd.sampler import sample_into
+
+        r = i % self.R
+        sample_into(self.logits[r], self.ids, self.ws, uniforms=self.uniforms[r], use_top_p=True, **self.params)
+
+
+def time_graph(case: Case, steps: int, warmup: int, repeats: int = 5):
+    """µs/step over graph replays of R captured steps; median of `repeats`."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(max(warmup, case.R)):
+            case.step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(case.R):
+            case.step(i)
+    torch.cuda.synchronize()
+    reps = max(1, math.ceil(steps / case.R))
+    for _ in range(max(1, warmup // case.R)):
+        g.replay()
+    torch.cuda.synchronize()
+    results = []
+    for _ in range(repeats):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            g.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        results.append(start.elapsed_time(stop) * 1000.0 / (reps * case.R))
+    return statistics.median(results), reps * case.R, results
+
+
+def time_eager(case: Case, steps: int):
+    """Host-inclusive µs per call (ctypes launch from Python, no graph)."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        case.step(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e6 / steps
+
+
+def cpu_baseline(name: str, budget_s: float = 20.0):
+    """The torch-CPU restatement of the reference sampler on this host's cores."""
+    import numpy as np
+    import torch
+
+    from oracle import torch_ref
+    from qedge_amd import workloads as W
+
+    w = W.make(name)
+    if w.dtype == "f32":
+        logits = torch.from_numpy(np.ascontiguousarray(w.logits))
+    else:
+        logits = torch.from_numpy(np.ascontiguousarray(w.logits).view(np.int16)).view(torch.bfloat16)
+    t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dt)
+    kw = dict(top_ks=t(w.top_k, torch.int32), rep=t(w.rep, torch.float32), pres=t(w.pres, torch.float32),
+              freq=t(w.freq, torch.float32), history=t(w.history, torch.int32))
+    T, P = t(w.temperature, torch.float32), t(w.top_p, torch.float32)
+    gen = torch.Generator().manual_seed(0)
+    times = []
+    with torch.inference_mode():
+        for i in range(2):
+            torch_ref.extended_forward(logits, T, P, use_top_p=True, generator=gen, **kw)
+        t_start = time.perf_counter()
+        while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+            t0 = time.perf_counter()
+            torch_ref.extended_forward(logits, T, P, use_top_p=True, generator=gen, **kw)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > budget_s and len(times) >= 3:
+                break
+        faithful = []
+        for i in range(3):
+            t0 = time.perf_counter()
+            torch_ref.reference_forward(logits, T, P, use_top_p=True, generator=gen)
+            faithful.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(w.nrows / med, 3),
+        "unit": "rows/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{name}: {len(times)} timed steps of B={w.nrows} after 2 warm-up steps, median; "
+                   f"torch-CPU restatement of the reference op sequence with top-k/top-p "
+                   f"(oracle/torch_ref.extended_forward), {torch.get_num_threads()} threads of "
+                   f"{os.cpu_count()} host CPUs"),
+        "ms_per_step": round(med * 1e3, 3),
+        "faithful_ms_per_step": round(statistics.median(faithful) * 1e3, 3),
+    }
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc, if a summary is committed."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default=WORKLOAD)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-b1", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the sampler on one GPU only: every row is independent, so N GPUs "
+              "would each run this same kernel on B/N rows; run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X)", file=sys.stderr)
+        return 2
+    from qedge_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    _log(f"device {torch.cuda.get_device_name(dev)}; staging {args.workload}")
+    case = Case(args.workload, dev)
+    _log(f"B={case.B} V={case.V} copies={case.R}; warmup {args.warmup}, steps {args.steps}")
+    torch.cuda.synchronize()
+    us, steps_done, reps = time_graph(case, args.steps, args.warmup)
+    _log(f"graph replay: {us:.3f} us/step (repeats {[round(r, 3) for r in reps]})")
+    eager_us = time_eager(case, min(args.steps, 500))
+    _log(f"eager (host-inclusive): {eager_us:.3f} us/call")
+
+    b1 = None
+    if not args.no_b1:
+        c1 = Case(B1_WORKLOAD, dev)
+        b1_us, _, _ = time_graph(c1, args.steps, args.warmup)
+        b1_eager = time_eager(c1, min(args.steps, 500))
+        b1 = {"workload": B1_WORKLOAD, "us_per_step": round(b1_us, 3), "eager_us_per_call": round(b1_eager, 3)}
+        _log(f"B=1 {B1_WORKLOAD}: {b1_us:.3f} us/step graph, {b1_eager:.3f} us/call eager")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("cpu baseline ...")
+        cpu = cpu_baseline(args.workload, args.cpu_budget)
+        _log(f"cpu baseline: {cpu['ms_per_step']} ms/step on {cpu['cores']} threads")
+
+    sec = us * 1e-6
+    achieved = case.alg_bytes / sec / 1e9
+    out = {
+        "metric": "sampled rows/s + HBM GB/s (B=64,V=248320 bf16); us/step at B=1",
+        "value": round(case.B / sec, 3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps_done,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1000.0, 6),
+        "us_per_step": round(us, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "B": case.B, "V": case.V, "logits": case.w.dtype,
+                   "algorithmic_bytes_per_step": case.alg_bytes, "rotating_copies": case.R,
+                   "timing": "HIP-graph replay, HIP events", "eager_us_per_call": round(eager_us, 3)},
+        "hbm_gbs": round(achieved, 3),
+        "b1": b1,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic_from_profile(args.workload)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -11,11 +11,12 @@
  * Sampling contract (shared by the kernels and the CPU oracle; ids are exact):
  *  - z = fp32(logit), then the history penalties below, one IEEE fp32 step each.
  *  - greedy rows (temperature <= 1e-5): first index of max z, NaN is maximum.
- *  - weights: exp(z/T) evaluated to a 24-bit mantissa M and exponent n
- *    (y = z*(log2 e / T) in double, n = floor(y), M from a fixed fp32
+ *  - sampling rows: q = z / T, one IEEE fp32 division (src/compute/sampler.py:32).
+ *  - weights: exp(q) evaluated to a 24-bit mantissa M and exponent n
+ *    (y = q*log2(e) in double, n = floor(y), M from a fixed fp32
  *    polynomial of y-n), scaled to a u64 relative to the row's largest n with
  *    a 40-octave window.
- *  - order: z descending, ties by ascending id.  top-k keeps z >= the k-th
+ *  - order: q descending, ties by ascending id.  top-k keeps q >= the k-th
  *    largest; top-p keeps the prefix whose exclusive mass <= floor(top_p*S)
  *    (exact 128-bit integers), S = mass of the top-k set.
  *  - draw: t = floor(u*W) over the kept mass W; kept tokens in ascending id,

@@ -23,17 +23,18 @@
  *      each step one IEEE fp32 operation:  z = z>0 ? z/rep : z*rep;
  *      z = z - freq*(float)c;  z = z - pres.
  *  R1  greedy row iff T <= 1e-5f: id = first index of max z (NaN is maximum).
- *  R2  order key: k_i = orderable bits of z_i (NaN -> lowest, -0 -> +0);
- *      rows are ordered by (k desc, id asc).  Dividing by T > 0 preserves the
- *      order of sampler.py:32, so this is the order torch.sort gives on the
- *      probabilities with ties taken in ascending id (sampler.py:35).
- *  R3  weights ("exp(z/T)" to 24 bits, free of any anchor):
- *        y_i = clamp((double)z_i * (LOG2E / (double)T), -2^30, 2^30)  (NaN -> -2^30)
+ *  R2  q_i = z_i / T, one IEEE fp32 division (sampler.py:32).  Order key:
+ *      k_i = orderable bits of q_i (NaN -> lowest, -0 -> +0); rows are ordered
+ *      by (k desc, id asc) -- the order torch.sort gives on the probabilities
+ *      (sampler.py:35), ties taken in ascending id.
+ *  R3  weights ("exp(q)" to 24 bits, free of any anchor):
+ *        y_i = clamp((double)q_i * LOG2E, -2^30, 2^30)  (NaN -> -2^30)
  *        n_i = floor(y_i), f_i = y_i - n_i,  P = poly((float)f_i) ~ 2^f in [1,2)
- *        M_i = 24-bit mantissa of P;  exp(z_i/T) ~= M_i * 2^(n_i-23)
+ *        M_i = 24-bit mantissa of P;  exp(q_i) ~= M_i * 2^(n_i-23)
  *      Row scale N = max n_i; window: w_i = M_i << (n_i - N + 40) if
  *      n_i >= N-40 else 0 (u64, exact).  p_i = w_i / sum(w).
- *  R4  top-k (E2): if 0 < k < V, kappa = key at rank k-1; keep k_i >= kappa.
+ *  R4  top-k (E2): if 0 < k < V, kappa = key at rank k-1; keep k_i >= kappa
+ *      (top-k after temperature, ties at the k-th value kept).
  *  R5  top-p (sampler.py:35-37 restated exactly): S = sum of w over the top-k
  *      set; Tp = floor(top_p * S) (exact 128-bit); walking the top-k set in
  *      order, keep a token iff its exclusive prefix mass <= Tp.  top_p >= 1
@@ -93,18 +94,18 @@ float qso_z_of_key(uint32_t k) {
   return u2f(u);
 }
 
-static inline double y_of(float z, double c) {
-  if (z != z) return -QS_YCLAMP;
-  double y = (double)z * c;
+static inline double y_of(float q) {
+  if (q != q) return -QS_YCLAMP;
+  double y = (double)q * QS_LOG2E;
   if (!(y >= -QS_YCLAMP)) y = -QS_YCLAMP;
   if (y > QS_YCLAMP) y = QS_YCLAMP;
   return y;
 }
 
-/* (n, M) such that exp(z/T) ~= M * 2^(n-23). */
-void qso_detexp(const float* z, int count, double c, int32_t* n_out, uint32_t* m_out) {
+/* (n, M) such that exp(q) ~= M * 2^(n-23). */
+void qso_detexp(const float* q, int count, int32_t* n_out, uint32_t* m_out) {
   for (int i = 0; i < count; ++i) {
-    double y = y_of(z[i], c);
+    double y = y_of(q[i]);
     double fl = floor(y);
     double f = y - fl;
     n_out[i] = (int32_t)fl;
@@ -200,17 +201,18 @@ static int64_t sample_row(const void* row, int dtype, int V, float T, float top_
     info->kept = 1;
     return arg;
   }
+  /* R2: q = z / T in place */
+  for (int i = 0; i < V; ++i) z[i] = z[i] / T;
   /* R3 weights */
-  double c = QS_LOG2E / (double)T;
   int32_t N = INT32_MIN;
   for (int i = 0; i < V; ++i) {
-    double y = y_of(z[i], c);
+    double y = y_of(z[i]);
     int32_t n = (int32_t)floor(y);
     if (n > N) N = n;
   }
   info->n_max = N;
   for (int i = 0; i < V; ++i) {
-    double y = y_of(z[i], c);
+    double y = y_of(z[i]);
     double fl = floor(y);
     int32_t n = (int32_t)fl;
     if (n >= N - QS_WINDOW) {
@@ -323,20 +325,21 @@ int qso_sample(const void* logits, int dtype, int64_t row_stride, int B, int V, 
   return status;
 }
 
-/* Weights of one row after penalties (R0, R3): outputs n, M, key per token. */
+/* One row after penalties and temperature (R0, R2, R3): per token z, q, key(q), n, M. */
 void qso_row_weights(const void* row, int dtype, int V, float T, const int32_t* hist, int H,
                      float rep, float pres, float freq, int32_t* n_out, uint32_t* m_out,
-                     uint32_t* key_out, float* z_out) {
+                     uint32_t* key_out, float* z_out, float* q_out) {
   int32_t* cnt = (int32_t*)calloc((size_t)V, sizeof(int32_t));
   int has_pen = 0;
   if (hist) for (int h = 0; h < H; ++h) if (hist[h] >= 0 && hist[h] < V) { cnt[hist[h]]++; has_pen = 1; }
-  double c = QS_LOG2E / (double)T;
   for (int i = 0; i < V; ++i) {
     float v = load_logit(row, dtype, i);
     if (has_pen) v = apply_penalty(v, cnt[i], rep, pres, freq);
     z_out[i] = v;
-    key_out[i] = qso_key(v);
-    double y = y_of(v, c);
+    float q = v / T;
+    q_out[i] = q;
+    key_out[i] = qso_key(q);
+    double y = y_of(q);
     double fl = floor(y);
     n_out[i] = (int32_t)fl;
     m_out[i] = mant24(qso_exp2_poly((float)(y - fl)));

@@ -38,7 +38,7 @@ def _load():
         lib.qso_sample.argtypes = [P, ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                    P, P, P, P, P, P, P, ctypes.c_int, P, P, P, P, ctypes.c_int]
         lib.qso_detexp.restype = None
-        lib.qso_detexp.argtypes = [P, ctypes.c_int, ctypes.c_double, P, P]
+        lib.qso_detexp.argtypes = [P, ctypes.c_int, P, P]
         lib.qso_exp2_poly.restype = ctypes.c_float
         lib.qso_exp2_poly.argtypes = [ctypes.c_float]
         lib.qso_key.restype = ctypes.c_uint32
@@ -47,7 +47,7 @@ def _load():
         lib.qso_z_of_key.argtypes = [ctypes.c_uint32]
         lib.qso_row_weights.restype = None
         lib.qso_row_weights.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_float, P, ctypes.c_int,
-                                        ctypes.c_float, ctypes.c_float, ctypes.c_float, P, P, P, P]
+                                        ctypes.c_float, ctypes.c_float, ctypes.c_float, P, P, P, P, P]
         lib.qso_u128_to_double.restype = ctypes.c_double
         lib.qso_u128_to_double.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         _lib = lib
@@ -112,14 +112,13 @@ def sample_workload(w, step: int = 0, want_probs: bool = False, threads: int | N
                   w.history, w.uniforms(step), want_probs=want_probs, threads=threads)
 
 
-def detexp(z: np.ndarray, temperature: float):
-    """(n, M) with exp(z/T) ~= M * 2**(n-23), per the contract's weight rule."""
+def detexp(q: np.ndarray):
+    """(n, M) with exp(q) ~= M * 2**(n-23), per the contract's weight rule."""
     lib = _load()
-    z = np.ascontiguousarray(z, dtype=np.float32)
-    n = np.zeros(z.size, np.int32)
-    m = np.zeros(z.size, np.uint32)
-    c = 1.4426950408889634074 / float(np.float32(temperature))
-    lib.qso_detexp(_ptr(z), z.size, c, _ptr(n), _ptr(m))
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n = np.zeros(q.size, np.int32)
+    m = np.zeros(q.size, np.uint32)
+    lib.qso_detexp(_ptr(q), q.size, _ptr(n), _ptr(m))
     return n, m
 
 
@@ -136,7 +135,7 @@ def z_of_key(k: int) -> float:
 
 
 def row_weights(row: np.ndarray, dtype: str, temperature: float, history=None, rep=1.0, pres=0.0, freq=0.0):
-    """Per-token (z, key, n, M) after penalties, as the contract defines them."""
+    """Per-token (z, q, key(q), n, M) after penalties and temperature, as the contract defines them."""
     lib = _load()
     row = np.ascontiguousarray(row)
     V = row.shape[0]
@@ -145,10 +144,11 @@ def row_weights(row: np.ndarray, dtype: str, temperature: float, history=None, r
     m = np.zeros(V, np.uint32)
     k = np.zeros(V, np.uint32)
     z = np.zeros(V, np.float32)
+    q = np.zeros(V, np.float32)
     lib.qso_row_weights(_ptr(row), 0 if dtype == "f32" else 1, V, float(temperature), _ptr(hist),
                         0 if hist is None else hist.size, float(rep), float(pres), float(freq),
-                        _ptr(n), _ptr(m), _ptr(k), _ptr(z))
-    return z, k, n, m
+                        _ptr(n), _ptr(m), _ptr(k), _ptr(z), _ptr(q))
+    return z, q, k, n, m
 
 
 def u128_to_double(x: int) -> float:

@@ -344,6 +344,7 @@ __device__ __forceinline__ float load_logit(const Args& a, int row, int i) {
   }
 }
 
+// q = (penalised logit) / T for a sampling row (one IEEE fp32 division).
 template <int DT>
 __device__ __forceinline__ float load_z(const Args& a, const RowParams& p, int row, int i) {
   float z = load_logit<DT>(a, row, i);
@@ -351,7 +352,7 @@ __device__ __forceinline__ float load_z(const Args& a, const RowParams& p, int r
     uint32_t c = hist_count(a, row, i);
     if (c) z = apply_penalty(z, c, p.rep, p.pres, p.freq);
   }
-  return z;
+  return z / p.T;
 }
 
 // Clear a row's state (the caller is the last reader of it in this call).
@@ -518,6 +519,10 @@ __global__ __launch_bounds__(kMainThreads) void k_main(Args a) {
         }
       }
     }
+    if (!p.greedy) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) z[v * VW + j] = z[v * VW + j] / p.T;
+    }
   }
 
   // ---- row maximum (greedy: NaN is maximum; sampling: NaN is minimum)
@@ -644,7 +649,7 @@ __global__ __launch_bounds__(kMainThreads) void k_main(Args a) {
     if (a.last_kernel == 1) clear_row(rs);
     return;
   }
-  const int N = octave_of(z_of_key((uint32_t)(mp >> 32)), kLog2e / (double)p.T);
+  const int N = octave_of(z_of_key((uint32_t)(mp >> 32)), kLog2e);
   if (tid == 0) rs->n_max = N;
   if (!fast_topk) {
     if (tid == 0) rs->status = kNeedsResolve;
@@ -692,7 +697,7 @@ __global__ __launch_bounds__(kMainThreads) void k_main(Args a) {
     __syncthreads();
     kend = (int)sh.counter;
   }
-  const double cT = kLog2e / (double)p.T;
+  const double cT = kLog2e;
   // each thread owns a contiguous run of sorted positions
   const int per = (kend + kMainThreads - 1) / kMainThreads;
   Acc loc = {0, 0, 0};
@@ -897,7 +902,7 @@ __global__ __launch_bounds__(kResolveThreads) void k_resolve(Args a) {
   }
   const RowParams p = row_params(a, row);
   const int N = rs->n_max;
-  const double cT = kLog2e / (double)p.T;
+  const double cT = kLog2e;
   // top-k: rank k-1 over all elements
   uint32_t kappa_k = 0u;
   Acc Sk;
@@ -1018,7 +1023,7 @@ __global__ __launch_bounds__(kMainThreads) void k_probs(Args a) {
     }
   } else {
     const int N = rs->n_max;
-    const double cT = kLog2e / (double)p.T;
+    const double cT = kLog2e;
     const u128 W = ((u128)rs->w_hi << 64) | rs->w_lo;
     const double Wd = u128_to_double(W);
     const uint32_t kp = rs->kappa_p, idp = rs->id_p;
