@@ -79,7 +79,8 @@ class Case:
         from qedge_amd.sampler import sample_into
 
         r = i % self.R
-        sample_into(self.logits[r], self.ids, self.ws, uniforms=self.uniforms[r], use_top_p=True, **self.params)
+        sample_into(self.logits[r], self.ids, self.ws, uniforms=self.uniforms[r], use_top_p=True,
+                    mass_rows=self.w.mass_rows, **self.params)
 
 
 def time_graph(case: Case, steps: int, warmup: int, repeats: int = 5):

@@ -42,9 +42,19 @@ extern "C" {
                                  (src/compute/model_runner.py:82,84-85) */
 #define QS_FLAG_USE_TOP_P 2u  /* apply top_p; without it top_p is ignored
                                  (src/compute/sampler.py:34,39-40) */
+#define QS_FLAG_NO_MASS_ROWS 4u /* host hint from the CPU-side parameters: every
+                                   sampling row has 0 < top_k <= QS_TOPK_FAST_MAX
+                                   (same kind of batch flag as use_top_p,
+                                   src/compute/model_runner.py:82-83); skips the
+                                   launch that serves top-k-off rows.  If such a
+                                   row is present anyway it is still resolved
+                                   exactly, by a slower path. */
 
 #define QS_TOPK_FAST_MAX 1024 /* top_k up to this value is resolved from
-                                 per-chunk candidates in the main kernel */
+                                 per-chunk candidates in one pass */
+#define QS_MAX_HISTORY 8192   /* longest token history per row (ids); the
+                                 reference's max_model_len is 8192
+                                 (src/config.py:49) */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int qs_version(void);

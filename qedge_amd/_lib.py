@@ -16,6 +16,7 @@ QS_DTYPE_F32 = 0
 QS_DTYPE_BF16 = 1
 QS_FLAG_ALL_GREEDY = 1
 QS_FLAG_USE_TOP_P = 2
+QS_FLAG_NO_MASS_ROWS = 4
 QS_TOPK_FAST_MAX = 1024
 
 EXPORTS = ("qs_version", "qs_last_error", "qs_workspace_bytes", "qs_workspace_init", "qs_sample", "qs_argmax")

@@ -55,8 +55,14 @@ def sample_into(logits: torch.Tensor, out_ids: torch.Tensor, workspace: Workspac
                 presence_penalties: torch.Tensor | None = None,
                 frequency_penalties: torch.Tensor | None = None, history: torch.Tensor | None = None,
                 uniforms: torch.Tensor | None = None, all_greedy: bool = False, use_top_p: bool = False,
-                out_probs: torch.Tensor | None = None, out_kept: torch.Tensor | None = None) -> torch.Tensor:
-    """Sample into caller-owned ``out_ids`` (int64 [B]); allocates nothing."""
+                mass_rows: bool = True, out_probs: torch.Tensor | None = None,
+                out_kept: torch.Tensor | None = None) -> torch.Tensor:
+    """Sample into caller-owned ``out_ids`` (int64 [B]); allocates nothing.
+
+    ``mass_rows`` is a host-side batch flag from the CPU parameters: False when
+    every sampling row has 0 < top_k <= QS_TOPK_FAST_MAX, which skips the launch
+    that serves top-k-off rows (such a row is still resolved exactly if present).
+    """
     if logits.dim() != 2 or logits.dtype not in _DTYPES or not logits.is_cuda:
         raise ValueError("logits must be a [B, V] float32/bfloat16 device tensor")
     if logits.stride(1) != 1:
@@ -71,7 +77,8 @@ def sample_into(logits: torch.Tensor, out_ids: torch.Tensor, workspace: Workspac
         raise ValueError("top_ks must be contiguous int32")
     if history is not None and (history.dtype != torch.int32 or not history.is_contiguous()):
         raise ValueError("history must be contiguous int32 [B, H]")
-    flags = (_lib.QS_FLAG_ALL_GREEDY if all_greedy else 0) | (_lib.QS_FLAG_USE_TOP_P if use_top_p else 0)
+    flags = ((_lib.QS_FLAG_ALL_GREEDY if all_greedy else 0) | (_lib.QS_FLAG_USE_TOP_P if use_top_p else 0)
+             | (0 if mass_rows else _lib.QS_FLAG_NO_MASS_ROWS))
     lib = _lib.load()
     rc = lib.qs_sample(
         ctypes.c_void_p(logits.data_ptr()), logits.stride(0), _DTYPES[logits.dtype], B, V,

@@ -105,6 +105,13 @@ class Workload:
     def uniforms(self, step: int) -> np.ndarray:
         return np.array([uniform_f32(self.seed, r, step) for r in self.rows], dtype=np.float32)
 
+    @property
+    def mass_rows(self) -> bool:
+        """Host-side batch flag: some sampling row has top-k off (or above the fast limit)."""
+        k = self.top_k.astype(np.int64)
+        fast = (k > 0) & (k <= 1024) & (k < self.V)
+        return bool(np.any((self.temperature > 1e-5) & ~fast))
+
     def logits_f32(self) -> np.ndarray:
         return self.logits if self.dtype == "f32" else bf16_to_f32(self.logits)
 

@@ -30,8 +30,8 @@ def run_gpu(w, device, step=0, want_probs=True, all_greedy=False, use_top_p=True
     probs = torch.empty((B, V), dtype=torch.float32, device=device) if want_probs else None
     kept = torch.empty(B, dtype=torch.int32, device=device) if want_probs else None
     logits = d.pop("logits")
-    sample_into(logits, ids, ws, uniforms=u, all_greedy=all_greedy, use_top_p=use_top_p, out_probs=probs,
-                out_kept=kept, **d)
+    sample_into(logits, ids, ws, uniforms=u, all_greedy=all_greedy, use_top_p=use_top_p, mass_rows=w.mass_rows,
+                out_probs=probs, out_kept=kept, **d)
     torch.cuda.synchronize()
     return (ids.cpu().numpy(), None if probs is None else probs.cpu().numpy(),
             None if kept is None else kept.cpu().numpy())
