@@ -120,7 +120,7 @@ class BatchSampler(nn.Module):
                 repetition_penalties: torch.Tensor | None = None,
                 presence_penalties: torch.Tensor | None = None,
                 frequency_penalties: torch.Tensor | None = None, history: torch.Tensor | None = None,
-                uniforms: torch.Tensor | None = None) -> torch.Tensor:
+                uniforms: torch.Tensor | None = None, mass_rows: bool = True) -> torch.Tensor:
         B, V = logits.shape
         if logits.stride(1) != 1:
             logits = logits.contiguous()
@@ -129,12 +129,13 @@ class BatchSampler(nn.Module):
         H = 0 if history is None else int(history.shape[1])
         ws = self.workspace(B, V, logits.dtype, H, logits.device)
         out = torch.empty(B, dtype=torch.int64, device=logits.device)
-        return sample_into(logits, out, ws, temperatures=temperatures[:B].contiguous(),
-                           top_ps=None if top_ps is None else top_ps[:B].contiguous(),
-                           top_ks=None if top_ks is None else top_ks[:B].contiguous(),
-                           repetition_penalties=repetition_penalties, presence_penalties=presence_penalties,
-                           frequency_penalties=frequency_penalties, history=history, uniforms=uniforms,
-                           all_greedy=all_greedy, use_top_p=use_top_p)
+        sl = lambda t: None if t is None else t[:B].contiguous()
+        return sample_into(logits, out, ws, temperatures=None if temperatures is None else sl(temperatures),
+                           top_ps=sl(top_ps), top_ks=sl(top_ks), repetition_penalties=sl(repetition_penalties),
+                           presence_penalties=sl(presence_penalties), frequency_penalties=sl(frequency_penalties),
+                           history=None if history is None else history[:B].contiguous(),
+                           uniforms=None if uniforms is None else uniforms[:B].contiguous(),
+                           all_greedy=all_greedy, use_top_p=use_top_p, mass_rows=mass_rows)
 
 
 def argmax_into(logits: torch.Tensor, out_ids: torch.Tensor, workspace: Workspace) -> torch.Tensor:
@@ -151,6 +152,30 @@ def argmax_into(logits: torch.Tensor, out_ids: torch.Tensor, workspace: Workspac
                              ctypes.c_void_p(out_ids.data_ptr()), ctypes.c_void_p(workspace.buf.data_ptr()),
                              workspace.nbytes, ctypes.c_void_p(_stream_handle(logits.device))))
     return out_ids
+
+
+def sample_gpu(sampler: "BatchSampler", logits: torch.Tensor | list[torch.Tensor], batch) -> torch.Tensor:
+    """One token per row: the role of ModelRunner._sample_gpu (src/compute/model_runner.py:77-93).
+
+    ``logits`` is a [B, V] tensor or a list of [1, V] rows (concatenated as at
+    model_runner.py:81); ``batch`` is a filled ``SamplingBatch`` whose host flags
+    pick the path: all-greedy rows take the argmax kernel (model_runner.py:84-85),
+    otherwise the sampler runs with the batch's device buffers (:87-92).
+    """
+    if isinstance(logits, (list, tuple)):
+        if not logits:
+            dev = batch.device
+            return torch.empty(0, dtype=torch.long, device=dev)
+        logits = torch.cat(list(logits), dim=0)
+    B, V = logits.shape
+    if batch.all_greedy:
+        if logits.stride(1) != 1:
+            logits = logits.contiguous()
+        ws = sampler.workspace(B, V, logits.dtype, 0, logits.device)
+        out = torch.empty(B, dtype=torch.int64, device=logits.device)
+        return argmax_into(logits, out, ws)
+    kw = batch.sampler_kwargs()
+    return sampler(logits, kw.pop("temperatures"), kw.pop("top_ps"), **kw)
 
 
 _default = None

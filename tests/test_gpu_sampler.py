@@ -1,0 +1,237 @@
+"""GPU parity of the HIP sampler against the CPU oracle: every id, surviving-set
+size and post-filter probability must be identical.  Needs an MI355X."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import contract
+from qedge_amd import workloads as W
+from qedge_amd.batch import SamplingBatch
+from qedge_amd.sampler import BatchSampler, Workspace, argmax_into, sample_gpu, sample_into
+from qedge_amd.sampling_params import SamplingParams
+from tests.devrun import run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev_logits(x, dtype, device, stride=None):
+    B, V = x.shape
+    if dtype == "f32":
+        full = np.zeros((B, stride or V), np.float32)
+        full[:, :V] = x
+        t = torch.from_numpy(full).to(device)
+    else:
+        full = np.zeros((B, stride or V), np.uint16)
+        full[:, :V] = x
+        t = torch.from_numpy(full.view(np.int16)).to(device).view(torch.bfloat16)
+    return t[:, :V]
+
+
+def _run(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hist=None, u=None,
+         use_top_p=True, mass_rows=True, stride=None, probs=True):
+    B, V = x.shape
+    lg = _dev_logits(x, dtype, device, stride)
+    t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)
+    H = 0 if hist is None else hist.shape[1]
+    ws = Workspace(B, V, lg.dtype, H, device)
+    ids = torch.empty(B, dtype=torch.int64, device=device)
+    pr = torch.empty((B, V), dtype=torch.float32, device=device) if probs else None
+    kept = torch.empty(B, dtype=torch.int32, device=device) if probs else None
+    sample_into(lg, ids, ws, temperatures=t(T, torch.float32), top_ps=t(P, torch.float32), top_ks=t(K, torch.int32),
+                repetition_penalties=t(rep, torch.float32), presence_penalties=t(pres, torch.float32),
+                frequency_penalties=t(freq, torch.float32), history=t(hist, torch.int32),
+                uniforms=t(u, torch.float32), use_top_p=use_top_p, mass_rows=mass_rows, out_probs=pr, out_kept=kept)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), None if pr is None else pr.cpu().numpy(), None if kept is None else kept.cpu().numpy()
+
+
+def _check(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hist=None, u=None, **kw):
+    ids, probs, kept = _run(x, dtype, device, T, P, K, rep, pres, freq, hist, u, **kw)
+    use_top_p = kw.get("use_top_p", True)
+    ref = contract.sample(x, dtype, T, P if use_top_p else None, K, rep, pres, freq, hist, u,
+                          want_probs=probs is not None)
+    np.testing.assert_array_equal(ids, ref.ids)
+    if probs is not None:
+        np.testing.assert_array_equal(kept, ref.kept)
+        np.testing.assert_array_equal(probs, ref.probs)
+    return ids
+
+
+# ---------------------------------------------------------------- the five workloads
+
+
+@pytest.mark.parametrize("name", W.WORKLOADS)
+def test_full_batch_ids(gpu, name):
+    w = W.make(name)
+    print(f"[full] {name} B={w.nrows}", flush=True)
+    ids, _, _ = run_gpu(w, gpu, want_probs=False)
+    ref = run_oracle(w, want_probs=False)
+    np.testing.assert_array_equal(ids, ref.ids)
+
+
+@pytest.mark.parametrize("name", W.WORKLOADS)
+def test_steps_match_oracle_and_repeat(gpu, name):
+    rows = {"hetero_b64_bf16": list(range(0, 64, 3)), "penalties_b256_bf16": [0, 77, 200],
+            "flat_topp_b1024_f32": [5, 600]}.get(name)
+    w = W.make(name, rows=rows)
+    print(f"[steps] {name}", flush=True)
+    for step in (1, 2):
+        ids, probs, kept = run_gpu(w, gpu, step=step)
+        ref = run_oracle(w, step=step)
+        np.testing.assert_array_equal(ids, ref.ids)
+        np.testing.assert_array_equal(kept, ref.kept)
+        np.testing.assert_array_equal(probs, ref.probs)
+        again, _, _ = run_gpu(w, gpu, step=step, want_probs=False)
+        np.testing.assert_array_equal(again, ids)
+
+
+# ---------------------------------------------------------------- edge cases
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("V", [777, 4096, 20011])
+def test_small_and_ragged_vocabularies(gpu, dtype, V):
+    rng = np.random.default_rng(V)
+    B = 7
+    x = (rng.standard_normal((B, V)) * rng.uniform(0.1, 3.0, (B, 1))).astype(np.float32)
+    x[1] = np.round(x[1] * 2) / 2  # ties
+    x[2, 5] = np.nan
+    x[3, :10] = -np.inf
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    T = np.array([0.0, 0.7, 1.0, 1.3, 0.5, 0.9, 2.0], np.float32)
+    P = np.array([0.9, 0.5, 1.0, 0.99, 1e-4, 0.8, 0.95], np.float32)
+    K = np.array([0, 5, 0, min(V - 1, 1500), 1, 40, 0], np.int32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] V={V} {dtype}", flush=True)
+    _check(xx, dtype, gpu, T, P, K, u=u)
+
+
+def test_padded_rows_and_no_top_p(gpu):
+    rng = np.random.default_rng(3)
+    B, V = 5, 30001
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    T = np.full(B, 0.8, np.float32)
+    P = np.full(B, 0.5, np.float32)
+    u = rng.random(B).astype(np.float32)
+    print("[edge] padded rows", flush=True)
+    _check(x, "f32", gpu, T, P, u=u, stride=V + 13)
+    _check(x, "f32", gpu, T, P, u=u, use_top_p=False)
+
+
+def test_penalties_with_padding_ids(gpu):
+    rng = np.random.default_rng(4)
+    B, V, H = 6, 50000, 3000
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    hist = rng.integers(-5, V + 5, (B, H)).astype(np.int32)
+    hist[0, :200] = 17  # one token many times
+    T = np.array([0.0, 0.8, 1.0, 0.6, 1.2, 0.9], np.float32)
+    P = np.array([1.0, 0.95, 0.7, 1.0, 0.9, 0.6], np.float32)
+    K = np.array([0, 0, 30, 0, 500, 2000], np.int32)
+    rep = rng.uniform(0.9, 1.4, B).astype(np.float32)
+    pres = rng.uniform(0.0, 1.0, B).astype(np.float32)
+    freq = rng.uniform(0.0, 0.5, B).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    print("[edge] penalties", flush=True)
+    _check(W.bf16_bits(x), "bf16", gpu, T, P, K, rep, pres, freq, hist, u)
+
+
+def test_mass_rows_without_the_mass_launch(gpu):
+    """A top-k-off row under the no-mass-rows hint is still exact (slower path)."""
+    rng = np.random.default_rng(5)
+    B, V = 3, 40000
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    T = np.ones(B, np.float32)
+    P = np.array([0.9, 0.9, 0.9], np.float32)
+    K = np.array([20, 0, 50], np.int32)
+    print("[edge] no-mass hint", flush=True)
+    _check(x, "f32", gpu, T, P, K, u=rng.random(B).astype(np.float32), mass_rows=False)
+
+
+def test_adversarial_layout_falls_back_exactly(gpu):
+    """Sorted logits put the whole top-k in one chunk: the candidate path must give up and stay exact."""
+    B, V = 2, 100000
+    x = np.sort(np.random.default_rng(6).standard_normal((B, V)).astype(np.float32), axis=1)[:, ::-1].copy()
+    T = np.ones(B, np.float32)
+    P = np.array([0.99, 1.0], np.float32)
+    K = np.array([1000, 700], np.int32)
+    print("[edge] adversarial", flush=True)
+    _check(x, "f32", gpu, T, P, K, u=np.array([0.3, 0.7], np.float32))
+
+
+def test_argmax_entry_point(gpu):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((9, 70000)).astype(np.float32)
+    x[2, [5, 600, 9000]] = 100.0
+    x[4, 33] = np.nan
+    lg = torch.from_numpy(x).to(gpu).to(torch.bfloat16)
+    ws = Workspace(9, 70000, torch.bfloat16, 0, gpu)
+    out = torch.empty(9, dtype=torch.int64, device=gpu)
+    argmax_into(lg, out, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), lg.float().cpu().argmax(dim=-1).numpy())
+
+
+# ---------------------------------------------------------------- module API and graphs
+
+
+def test_batch_sampler_module_and_runner(gpu):
+    V = 248320
+    w = W.make("hetero_b64_bf16", rows=list(range(0, 64, 5)))
+    params = []
+    for r in range(w.nrows):
+        k = int(w.top_k[r])
+        params.append(SamplingParams(temperature=float(w.temperature[r]), top_p=float(w.top_p[r]),
+                                     top_k=None if k == 0 else k, seed=1000 + r))
+    batch = SamplingBatch(w.nrows, V, gpu)
+    batch.fill(params, step=3)
+    lg = torch.from_numpy(np.ascontiguousarray(w.logits).view(np.int16)).to(gpu).view(torch.bfloat16)
+    ids = sample_gpu(BatchSampler(), [lg[i:i + 1] for i in range(w.nrows)], batch)
+    torch.cuda.synchronize()
+    u = batch.uniforms[: w.nrows].cpu().numpy()
+    ref = contract.sample(w.logits, "bf16", batch.temperatures[: w.nrows].cpu().numpy(),
+                          batch.top_ps[: w.nrows].cpu().numpy(), batch.top_ks[: w.nrows].cpu().numpy(), uniforms=u)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref.ids)
+    # all-greedy batch: the argmax path
+    batch.fill([SamplingParams() for _ in range(w.nrows)])
+    g = sample_gpu(BatchSampler(), lg, batch)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(g.cpu().numpy(), lg.float().cpu().argmax(dim=-1).numpy())
+
+
+def test_graph_replays_match_eager(gpu):
+    w = W.make("hetero_b64_bf16")
+    lg = torch.from_numpy(np.ascontiguousarray(w.logits).view(np.int16)).to(gpu).view(torch.bfloat16)
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to(device=gpu, dtype=dt)
+    T, P, K = t(w.temperature, torch.float32), t(w.top_p, torch.float32), t(w.top_k, torch.int32)
+    U = [t(w.uniforms(s), torch.float32) for s in range(3)]
+    ws = Workspace(w.nrows, w.V, torch.bfloat16, 0, gpu)
+    outs = [torch.empty(w.nrows, dtype=torch.int64, device=gpu) for _ in range(3)]
+
+    def steps():
+        for s in range(3):
+            sample_into(lg, outs[s], ws, temperatures=T, top_ps=P, top_ks=K, uniforms=U[s], use_top_p=True,
+                        mass_rows=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        steps()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    eager = [o.cpu().numpy().copy() for o in outs]
+    ref = [contract.sample_workload(w, step=s).ids for s in range(3)]
+    for s in range(3):
+        np.testing.assert_array_equal(eager[s], ref[s])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        steps()
+    for rep in range(4):
+        for o in outs:
+            o.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for s in range(3):
+            np.testing.assert_array_equal(outs[s].cpu().numpy(), eager[s])
+        steps()  # eager work between replays
+        torch.cuda.synchronize()
