@@ -177,6 +177,32 @@ def cpu_baseline(name: str, budget_s: float = 20.0):
     }
 
 
+def counter_run(case: Case, steps: int, calib_mib: int = 1024, calib_runs: int = 4) -> dict:
+    """Short eager run for hardware-counter passes (rocprofv3 --pmc).
+
+    ``steps`` sampler calls, each on a different logits copy, then
+    ``calib_runs`` plain device copies of ``calib_mib`` MiB (torch's copy
+    kernel): their counters per dispatch are the scale that turns the
+    sampler's counters into HBM bytes.
+    """
+    import torch
+
+    for i in range(3):
+        case.step(i)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        case.step(3 + i)
+    torch.cuda.synchronize()
+    n = calib_mib << 18  # float32 elements
+    src = torch.empty(n, dtype=torch.float32, device=case.ids.device).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(calib_runs):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"mode": "counters", "workload": case.name, "sampler_calls": steps + 3,
+            "calibration_copy_bytes": n * 4, "calibration_runs": calib_runs}
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch measured by rocprofv3 --pmc, if a summary is committed."""
     path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
@@ -195,6 +221,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b1", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--counters", type=int, default=0, metavar="N",
+                    help="only run N eager sampler calls and a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the sampler on one GPU only: every row is independent, so N GPUs "
@@ -212,6 +240,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     _log(f"device {torch.cuda.get_device_name(dev)}; staging {args.workload}")
     case = Case(args.workload, dev)
+    if args.counters > 0:
+        print(json.dumps(counter_run(case, args.counters)), flush=True)
+        return 0
     _log(f"B={case.B} V={case.V} copies={case.R}; warmup {args.warmup}, steps {args.steps}")
     torch.cuda.synchronize()
     us, steps_done, reps = time_graph(case, args.steps, args.warmup)
