@@ -5,24 +5,31 @@
 // greedy argmax sites (src/compute/model_runner.py:85,353).  The arithmetic
 // contract is stated in include/qsampler.h; ids are exact integers.
 //
-// One kernel does the sampling: grid (G chunks, B rows), 256 threads (4 waves
-// of 64).  Each workgroup streams one chunk of a row into registers once
-// (16-byte loads), applies the history penalties from an LDS table and then
-// takes the path of its row:
-//   greedy row   local argmax, one 64-bit atomic max per workgroup; the last
-//                workgroup to arrive publishes the id.
-//   top-k row    (0 < k <= QS_TOPK_FAST_MAX) each workgroup emits the tokens
-//                above a threshold taken from its per-thread maxima; the last
-//                workgroup merges them in LDS and resolves top-k, top-p and the
-//                draw exactly.
-//   mass row     (top-k off) the workgroups of the row cooperate through row
-//                barriers: row maximum; fixed-point mass histograms over
-//                y = q*log2(e) (two levels) that bracket the top-p cut; an
-//                exact resolution of the bracketed tokens; the draw from
-//                per-chunk kept masses.  The chunk data stay in registers.
+// Grid (G chunks, B rows), 256 threads (4 waves of 64); each workgroup streams
+// one chunk of 8192 logits of a row into registers once (16-byte loads) and
+// applies the history penalties from an LDS table.  Two launches run side by
+// side (the second on a side stream):
+//   main launch  greedy rows: local argmax, one 64-bit atomic max per
+//                workgroup, the last workgroup to arrive publishes the id.
+//                top-k rows (0 < k <= QS_TOPK_FAST_MAX): every workgroup
+//                writes the tokens at or above a threshold taken from its
+//                per-thread maxima, in id order, to its own region; the last
+//                workgroup gathers the regions into registers (eight tokens per
+//                thread, still in id order) and resolves top-k, top-p and the
+//                draw with register radix selects over 256-bin LDS histograms.
+//   mass launch  rows with top-k off.  Every workgroup writes the tokens
+//                within 40 octaves of its own maximum; one row barrier
+//                exchanges the row maximum and the counts.  A peaked row (few
+//                such tokens) is then resolved by one workgroup like a top-k
+//                row.  A flat row stays cooperative: exact weights, per-bin
+//                masses, a second row barrier for the global histogram and the
+//                total mass, the bracket of bins holding the top-p boundary,
+//                the bracketed tokens listed; the last workgroup to arrive
+//                resolves the boundary exactly, finds the chunk holding the
+//                draw and re-reads that chunk to locate the token in id order.
 //   fallback     a single workgroup resolves the row exactly from global
-//                memory (rows with large k, candidate overflow, a missed
-//                bracket).  Slow, and rare on real logits.
+//                memory (large k, a candidate overflow, an incomplete
+//                candidate set, a bracket overflow).  Slow, rare on real logits.
 // Cross-workgroup data are written with device-coherent stores or atomics and
 // read with device-coherent loads; ordering comes from s_waitcnt before a
 // relaxed counter update.  No release/acquire fences: on this part they write
@@ -45,19 +52,40 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+constexpr int kEPT = 32;                          // logits per thread
+constexpr int kCH = kThreads * kEPT;              // logits per chunk (workgroup)
 constexpr int kWindow = 40;
 constexpr double kYClamp = 1073741824.0;  // 2^30
 constexpr double kLog2e = 1.4426950408889634074;
 constexpr int kTopkFast = QS_TOPK_FAST_MAX;
-constexpr int kBlockCand = 256;     // candidate slots per (row, workgroup) in the workspace
-constexpr int kMergeCap = 4096;     // candidates the finishing workgroup merges in LDS
-constexpr int kBins = 256;          // mass histogram bins per level
-constexpr int kBracketCap = 2048;   // bracketed tokens resolved exactly in LDS
-constexpr int kMaxChunks = 256;     // chunks per row (G)
+constexpr int kGatherPer = 32;                    // region entries one finishing thread loads
+constexpr int kRegionTotal = kThreads * kGatherPer;  // G * R <= this
+constexpr int kFinPer = 16;                       // merged candidates per thread
+constexpr int kFinCap = kThreads * kFinPer;       // merged candidates per row
+constexpr int kBins = 256;                        // histogram bins
+constexpr int kListCap = kFinCap;                 // bracket entries per row (flat mass rows)
+constexpr int kHash = 1024;                       // bracketed tokens per chunk (flat mass rows)
+constexpr int kMaxChunks = 256;                   // chunks per row (G)
 constexpr int kMaxHistory = QS_MAX_HISTORY;
 constexpr u32 kSpinLimit = 1u << 21;
 
-enum : u32 { kStFallback = 1u, kStTimeout = 2u, kStOverflow = 4u };
+enum : u32 { kStFallback = 1u, kStTimeout = 2u, kStOverflow = 4u, kStList = 8u };
+// Reasons for a fallback to resolve_single, recorded in RowCtl::why.
+enum : u32 {
+  kWhyRegion = 1u,      // a workgroup's region overflowed
+  kWhyMerge = 2u,       // more merged candidates than kFinCap
+  kWhyFewer = 3u,       // fewer merged candidates than k
+  kWhyKSelect = 4u,     // the k-select found no value
+  kWhyIncomplete = 5u,  // a token left out could be in the top-k set
+  kWhyTopP = 6u,        // the top-p select found no value
+  kWhyList = 11u,       // flat row: more bracketed tokens than kListCap
+  kWhyAbove = 12u,      // flat row: mass above the bracket exceeds the target
+  kWhyBracket = 13u,    // flat row: the boundary is not inside the bracket
+  kWhyTie = 14u,        // flat row: the tie select found no value
+  kWhyOwner = 15u,      // flat row: no chunk holds the draw target
+  kWhyTimeout = 16u,    // a row barrier gave up waiting
+  kWhyLargeK = 17u,     // top_k above QS_TOPK_FAST_MAX
+};
 
 // Per-row control block.  The first 64 bytes are counters that every call
 // leaves at zero; the rest holds the last call's result for k_probs.
@@ -65,41 +93,44 @@ struct __attribute__((aligned(256))) RowCtl {
   u64 pack;        // greedy: max of (gkey << 32 | ~id)
   u32 arrive;      // workgroups done
   u32 bar;         // row barrier counter
-  u32 cand_n;      // top-k candidates appended
-  u32 tau;         // max per-workgroup candidate threshold
   u32 kmax;        // mass rows: max key(q)
-  u32 nkmin;       // mass rows: ~min key(q)
+  u32 nkmin;       // mass rows: ~min key(q) over non-NaN tokens
   u32 status;      // kSt* flags
-  u32 brk_n;       // bracketed tokens appended
-  u32 brk_kmax;    // max key among bracketed tokens
-  u32 brk_nkmin;   // ~min key among bracketed tokens
+  u32 cand_n;      // mass rows: tokens written to the regions
+  u32 list_n;      // mass rows: bracketed tokens listed
   u32 probs_arrive;
   u32 probs_kept;
-  u32 nout;        // top-k rows: max key among tokens no workgroup emitted
-  u32 pad0;
+  u32 pad0[5];
   long long chosen;
   u64 w_lo, w_hi;  // kept mass W
+  u64 tp_lo, tp_hi;  // flat mass rows: floor(top_p * S)
   int n_max;       // row scale N
   u32 kappa_p, id_p;  // kept iff key > kappa_p || (key == kappa_p && id <= id_p)
   u32 greedy;
-  u32 path;        // how the row was resolved: 0 greedy, 1 top-k, 2 mass, 3 single workgroup
-  u32 pad1[37];
+  u32 path;        // 0 greedy, 1 top-k, 2 flat mass row, 3 single workgroup, 4 peaked mass row
+  u32 flat_blo;    // flat mass rows: lowest bin of the bracket
+  u32 why;         // why the last fallback to resolve_single was taken (kWhy*), 0 if none
+  u32 pad1[31];
 };
 static_assert(sizeof(RowCtl) == 256, "row control block is 256 bytes");
 constexpr int kCtlZeroWords = 16;
 
-// Per-(row, workgroup) published values of a mass row.
+// Per-(row, workgroup) published values.
 struct __attribute__((aligned(64))) Slot {
-  u64 s_lo, s_hi;  // exact mass of the chunk (plain draw) or the mass above the bracket
-  u32 nb;          // bracketed tokens in the chunk
-  u32 pad[11];
+  u64 s_lo, s_hi;  // mass rows: exact mass of the chunk
+  u64 a_lo, a_hi;  // flat mass rows: exact mass of the chunk's tokens above the bracket
+  u32 nb;          // tokens written to the region (0xffffffff: more than fit)
+  u32 tau;         // top-k rows: the region's threshold (z key)
+  u32 below;       // top-k rows: largest z key below tau in the chunk
+  u32 nbr;         // flat mass rows: bracketed tokens of the chunk
+  u32 pad[4];
 };
 static_assert(sizeof(Slot) == 64, "slot is 64 bytes");
 
 struct Args {
   const void* logits;
   long long row_stride;
-  int B, V, H, G, CH, seg_cap, Hpad;
+  int B, V, H, G, R, logR, seg_cap, Hpad;
   u32 flags;
   const float* temperature;
   const float* top_p;
@@ -113,18 +144,17 @@ struct Args {
   float* out_probs;
   int* out_kept;
   RowCtl* ctl;
-  u64* cand;   // [B, G, kBlockCand]
-  u64* mhist;  // [B, 2, kBins]
-  u64* brk;    // [B, kBracketCap]
+  u64* cand;   // [B, G, R] region entries (key << 32 | id)
+  u64* mhist;  // [B, kBins] global mass histogram (flat mass rows)
+  u64* list;   // [B, kListCap] bracket entries (key << 32 | chunk << 16 | count), flat mass rows
   Slot* slots; // [B, G]
   u64* trace;  // per-workgroup phase timestamps (trace builds only)
 };
 
 #ifdef QS_TRACE
-#define QS_TR(i)                                                                          \
-  do {                                                                                    \
-    if (a.trace && threadIdx.x == 0)                                                      \
-      a.trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 16 + (i)] = wall_clock64(); \
+#define QS_TR(i)                                                             \
+  do {                                                                       \
+    if (a.trace && threadIdx.x == 0) a.trace[(size_t)sc.tslot * 16 + (i)] = wall_clock64(); \
   } while (0)
 #else
 #define QS_TR(i) \
@@ -134,6 +164,13 @@ struct Args {
 
 // ---------------------------------------------------------------- memory model
 
+// Workgroup barrier for LDS traffic only: outstanding global loads stay in flight.
+__device__ __forceinline__ void lds_sync() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 // Wait until this thread's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_mem() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -209,6 +246,26 @@ __device__ __forceinline__ u64 weight_y(double y, int N) {
   return (u64)mant24(exp2_poly((float)(y - fl))) << (n - N + kWindow);
 }
 __device__ __forceinline__ u64 weight_of(float q, int N) { return weight_y(y_of(q), N); }
+// The weight packed in 32 bits: (n - N + 40) << 24 | M, 0 for weight 0.
+__device__ __forceinline__ u32 wpack_y(double y, int N) {
+  const double fl = floor(y);
+  const int n = (int)fl;
+  if (n < N - kWindow) return 0u;
+  return ((u32)(n - N + kWindow) << 24) | mant24(exp2_poly((float)(y - fl)));
+}
+__device__ __forceinline__ u32 wpack(float q, int N) { return wpack_y(y_of(q), N); }
+__device__ __forceinline__ u64 wunpack(u32 wp) { return wp ? (u64)(wp & 0xffffffu) << (wp >> 24) : 0ull; }
+// Smallest non-NaN key whose octave floor(y) is at least n0 (keys at or above
+// it are exactly the tokens inside a window that starts at octave n0).
+__device__ __forceinline__ u32 window_key(int n0) {
+  if ((double)n0 <= -kYClamp) return 1u;
+  if ((double)n0 > kYClamp) return 0xffffffffu;
+  u32 k = skey((float)((double)n0 / kLog2e));
+  if (k == 0u) k = 1u;
+  for (int it = 0; it < 64 && k > 1u && floor(y_of(f_of_key(k - 1u))) >= (double)n0; ++it) --k;
+  for (int it = 0; it < 64 && k < 0xffffffffu && floor(y_of(f_of_key(k))) < (double)n0; ++it) ++k;
+  return k;
+}
 // floor(x * f) for f in [0, 1] given as fp32, x < 2^104.
 __device__ __forceinline__ u128 mul_frac(u128 x, float f) {
   if (!(f > 0.0f)) return 0;
@@ -250,6 +307,10 @@ __device__ __forceinline__ float apply_penalty(float z, u32 c, float rep, float 
 }
 __device__ __forceinline__ float bf16_to_f32(u32 h) { return __uint_as_float(h << 16); }
 __device__ __forceinline__ u128 mk128(u64 lo, u64 hi) { return ((u128)hi << 64) | lo; }
+// Values the same in every lane, moved to scalar registers.
+__device__ __forceinline__ u32 uni(u32 v) { return (u32)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ u64 uni64(u64 v) { return ((u64)uni((u32)(v >> 32)) << 32) | uni((u32)v); }
+__device__ __forceinline__ u128 uni128(u128 v) { return mk128(uni64((u64)v), uni64((u64)(v >> 64))); }
 __device__ __forceinline__ int pow2_ceil(int n) {
   int p = 1;
   while (p < n) p <<= 1;
@@ -293,11 +354,12 @@ __device__ __forceinline__ RowParams row_params(const Args& a, int row) {
 // ---------------------------------------------------------------- block utils
 
 struct Scratch {   // static LDS
-  u64 w[3 * kWaves + 4];  // find_bin, lds_select results
+  u64 w[20];              // [12, 15]: find_bin results; [8, 20): select results
   u32 u[8];
   u32 v[kWaves][8];       // per-wave partials of the block collectives
   int i[8];               // find_bin
-  u32 r[8];               // results and counters of the callers
+  u32 r[16];              // results and counters of the callers
+  u32 tslot;              // trace builds: this workgroup's row of time stamps
 };
 
 // ---- wave64 collectives on DPP (row_shr, quad_perm, mirrors, row_bcast):
@@ -488,7 +550,31 @@ __device__ __forceinline__ void bitonic_i32(int* s, int n) {
   }
 }
 
-// ---------------------------------------------------------------- LDS radix select
+// Maxima of up to three u32 over the workgroup, one LDS exchange.
+__device__ __forceinline__ void block_max3(u32& a0, u32& a1, u32& a2, Scratch& s) {
+  a0 = wave_max(a0);
+  a1 = wave_max(a1);
+  a2 = wave_max(a2);
+  const int wv = threadIdx.x >> 6;
+  if (lane_id() == 0) {
+    s.v[wv][0] = a0;
+    s.v[wv][1] = a1;
+    s.v[wv][2] = a2;
+  }
+  __syncthreads();
+  u32 r0 = 0, r1 = 0, r2 = 0;
+  for (int i = 0; i < kWaves; ++i) {
+    r0 = s.v[i][0] > r0 ? s.v[i][0] : r0;
+    r1 = s.v[i][1] > r1 ? s.v[i][1] : r1;
+    r2 = s.v[i][2] > r2 ? s.v[i][2] : r2;
+  }
+  __syncthreads();
+  a0 = r0;
+  a1 = r1;
+  a2 = r2;
+}
+
+// ---------------------------------------------------------------- register radix select
 
 struct SelLds {  // one 8-bit digit level of a radix select
   u32 cnt[256];
@@ -497,102 +583,128 @@ struct SelLds {  // one 8-bit digit level of a radix select
 };
 
 struct SelOut {
-  u32 val;      // the selected 32-bit order value
-  Acc before;   // members strictly before it in the scan order (count, mass)
+  u32 val;      // the selected 32-bit value
+  Acc before;   // members ordered before it (count, mass)
   Acc at;       // members equal to it
   bool ok;      // false if the target is not below the members' total
 };
 
-// Over members i in [0, n) (in(i)), ordered by the 32-bit value val(i)
-// descending (DESC) or ascending, find the value at which the running count
-// (or, BY_MASS, the running sum of weight(i)) first exceeds `target`.
-// 8-bit digits from the highest bit where members differ; all threads call it.
-template <bool BY_MASS, bool DESC, typename ValF, typename InF, typename WF>
-__device__ __forceinline__ SelOut lds_select(int n, ValF val, InF in, WF weight, u128 target, SelLds& L,
-                                             Scratch& sc) {
+// Over the members (bit j of memb) of every thread's E values val[j], ordered
+// by value descending, the value at which the running count (or, BY_MASS, the
+// running weight wunpack(wp[j])) first exceeds `target`.  With CNT, member j
+// stands for mult[j] tokens of that value.  8-bit digits from the highest bit
+// where members differ; the histogram alternates between the two buffers
+// L[0], L[1].  All threads call it.
+template <bool BY_MASS, int E, bool CNT = false>
+__device__ __forceinline__ SelOut reg_select(const u32 (&val)[E], u32 memb, const u32 (&wp)[E], u128 target,
+                                             SelLds* L, Scratch& sc, const u32* mult = nullptr) {
   static_assert(kThreads == 256, "one digit bin per thread");
   const int tid = threadIdx.x;
-  // highest bit where the members' values differ
-  u32 first = 0u, any = 0u, diff = 0u;
-  {
-    u32 mx = 0u, mn = 0xffffffffu;
-    for (int i = tid; i < n; i += kThreads) {
-      if (in(i)) {
-        const u32 v = val(i);
-        mx = v > mx ? v : mx;
-        mn = v < mn ? v : mn;
-        any = 1u;
-      }
+  u32 mx = 0u, nmn = 0u, any = memb ? 1u : 0u;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    if ((memb >> j) & 1u) {
+      mx = val[j] > mx ? val[j] : mx;
+      nmn = ~val[j] > nmn ? ~val[j] : nmn;
     }
-    mx = block_max_u32(mx, sc);
-    mn = ~block_max_u32(~mn, sc);
-    any = block_max_u32(any, sc);
-    first = mn;
-    diff = mx ^ mn;
   }
+  block_max3(mx, nmn, any, sc);
+  mx = uni(mx);
+  nmn = uni(nmn);
+  any = uni(any);
+  target = uni128(target);
   SelOut out;
   out.before = Acc{0, 0, 0};
   out.at = Acc{0, 0, 0};
-  out.val = first;
+  out.val = ~nmn;
   out.ok = any != 0u;
   if (!any) return out;
+  const u32 first = ~nmn, diff = mx ^ first;
+  if (diff == 0u) {
+    // one value: every member is at it
+    Acc loc = {0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const u32 n = CNT ? mult[j] : 1u;
+      if ((memb >> j) & 1u) loc = acc_add(loc, acc_of(BY_MASS ? (u128)wunpack(wp[j]) * n : (u128)0, n));
+    }
+    out.at = block_sum_acc(loc, sc);
+    const u128 sz = BY_MASS ? acc_mass(out.at) : (u128)out.at.c;
+    out.ok = target < sz;
+    return out;
+  }
   int top = 31;
-  while (top > 0 && !((diff >> top) & 1u)) --top;
-  // the bits above `top` are common to all members: they start the prefix
+  while (!((diff >> top) & 1u)) --top;
   u32 prefix = (top == 31) ? 0u : (first & ~((2u << top) - 1u));
   u32 mask = (top == 31) ? 0u : ~((2u << top) - 1u);
   int hi = top;
-  for (;;) {
+  for (int lv = 0;; ++lv) {
+    SelLds& H = L[lv & 1];
     const int lo = hi >= 7 ? hi - 7 : 0;
-    const int width = hi - lo + 1;
-    const u32 dmask = (1u << width) - 1u;
-    L.cnt[tid] = 0u;
+    const u32 dmask = (1u << (hi - lo + 1)) - 1u;
+    H.cnt[tid] = 0u;
     if (BY_MASS) {
-      L.mlo[tid] = 0ull;
-      L.mhi[tid] = 0ull;
+      H.mlo[tid] = 0ull;
+      H.mhi[tid] = 0ull;
     }
+    // result slots alternate with the level, so no barrier is needed between
+    // one level's reads and the next level's writes
+    const int rs = 2 * (lv & 1), ws = 8 + 6 * (lv & 1);
+    if (tid == 0) sc.r[rs] = 0xffffffffu;
     __syncthreads();
-    for (int i = tid; i < n; i += kThreads) {
-      if (!in(i)) continue;
-      const u32 v = val(i);
-      if ((v & mask) != prefix) continue;
-      const u32 d = (v >> lo) & dmask;
-      atomicAdd(&L.cnt[d], 1u);
-      if (BY_MASS) {
-        const u64 w = weight(i);
-        if (w) {
-          atomicAdd(&L.mlo[d], w & 0xffffffffull);
-          atomicAdd(&L.mhi[d], w >> 32);
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      if (((memb >> j) & 1u) && (val[j] & mask) == prefix) {
+        const u32 d = (val[j] >> lo) & dmask;
+        const u32 n = CNT ? mult[j] : 1u;
+        atomicAdd(&H.cnt[d], n);
+        if (BY_MASS) {
+          // unpacked here, not hoisted out of the level loop (registers)
+          u32 wj = wp[j];
+          asm volatile("" : "+v"(wj));
+          const u64 w = wunpack(wj);
+          if (w) {
+            atomicAdd(&H.mlo[d], (w & 0xffffffffull) * n);
+            atomicAdd(&H.mhi[d], (w >> 32) * n);
+          }
         }
       }
     }
     __syncthreads();
-    // scan the bins in order: thread t takes bin (DESC ? 255 - t : t)
-    const int b = DESC ? 255 - tid : tid;
+    // scan the bins from the top: thread t takes bin 255 - t
+    const int b = 255 - tid;
     const bool live = b <= (int)dmask;
     Acc mine = {0, 0, 0};
     if (live) {
-      mine.c = L.cnt[b];
-      if (BY_MASS) mine = acc_of(mk128(L.mlo[b], 0) + ((u128)L.mhi[b] << 32), L.cnt[b]);
+      mine.c = H.cnt[b];
+      if (BY_MASS) mine = acc_of(mk128(H.mlo[b], 0) + ((u128)H.mhi[b] << 32), H.cnt[b]);
     }
-    Acc tot;
-    const Acc ex = block_scan_acc(mine, sc, &tot);
+    Acc ex;
+    if (BY_MASS) {
+      Acc tot;
+      ex = block_scan_acc(mine, sc, &tot);
+    } else {
+      u32 tot;
+      ex = acc_of(0, block_scan_u32(mine.c, sc, &tot));
+    }
     const u128 lo_m = BY_MASS ? acc_mass(ex) : (u128)ex.c;
     const u128 sz = BY_MASS ? acc_mass(mine) : (u128)mine.c;
-    if (tid == 0) sc.r[0] = 0xffffffffu;
-    __syncthreads();
     if (live && sz > 0 && target >= lo_m && target < lo_m + sz) {
-      sc.r[0] = (u32)b;
-      sc.w[3 * kWaves] = ex.lo;
-      sc.w[3 * kWaves + 1] = ex.hi;
-      sc.w[3 * kWaves + 2] = ex.c;
-      sc.w[3 * kWaves + 3] = ((u64)mine.c << 32);
+      sc.r[rs] = (u32)b;
+      sc.r[rs + 1] = mine.c;
+      sc.w[ws] = ex.lo;
+      sc.w[ws + 1] = ex.hi;
+      sc.w[ws + 2] = ex.c;
+      sc.w[ws + 3] = mine.lo;
+      sc.w[ws + 4] = mine.hi;
     }
     __syncthreads();
-    const u32 d = sc.r[0];
-    const Acc bex = {sc.w[3 * kWaves], sc.w[3 * kWaves + 1], (u32)sc.w[3 * kWaves + 2]};
-    __syncthreads();
+    const u32 d = uni(sc.r[rs]);
+    const u32 dcnt = uni(sc.r[rs + 1]);
+    const Acc bex = {uni64(sc.w[ws]), uni64(sc.w[ws + 1]), uni((u32)sc.w[ws + 2])};
+    const Acc bat = {uni64(sc.w[ws + 3]), uni64(sc.w[ws + 4]), dcnt};
     if (d == 0xffffffffu) {
+      __syncthreads();
       out.ok = false;
       return out;
     }
@@ -601,9 +713,19 @@ __device__ __forceinline__ SelOut lds_select(int n, ValF val, InF in, WF weight,
     prefix |= d << lo;
     mask |= dmask << lo;
     if (lo == 0) {
-      // the bin of the last level holds exactly the members equal to prefix
-      out.at.c = L.cnt[d];
-      if (BY_MASS) out.at = acc_of(mk128(L.mlo[d], 0) + ((u128)L.mhi[d] << 32), L.cnt[d]);
+      out.at = bat;
+      __syncthreads();
+      break;
+    }
+    if (dcnt == 1u) {
+      // a single member left: its value
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < E; ++j)
+        if (((memb >> j) & 1u) && (val[j] & mask) == prefix) sc.r[4] = val[j];
+      __syncthreads();
+      prefix = uni(sc.r[4]);
+      out.at = bat;
       __syncthreads();
       break;
     }
@@ -612,6 +734,7 @@ __device__ __forceinline__ SelOut lds_select(int n, ValF val, InF in, WF weight,
   out.val = prefix;
   return out;
 }
+
 
 // ---------------------------------------------------------------- row sync
 
@@ -645,12 +768,20 @@ __device__ __forceinline__ bool arrive_last(RowCtl* c, u32 G, Scratch& s) {
   return last;
 }
 
-// Called by the last workgroup of the row: counters and histograms to zero.
-__device__ __forceinline__ void reset_row(const Args& a, int row) {
+// Called by the last workgroup of the row: counters (and the row's mass
+// histogram, if it was used) to zero.
+__device__ __forceinline__ void reset_row(const Args& a, int row, bool hist = false) {
   u32* w = (u32*)(a.ctl + row);
   if (threadIdx.x < kCtlZeroWords) stc(&w[threadIdx.x], 0u);
-  u64* h = a.mhist + (size_t)row * 2 * kBins;
-  for (int i = threadIdx.x; i < 2 * kBins; i += kThreads) stc(&h[i], 0ull);
+  if (hist) {
+    u64* h = a.mhist + (size_t)row * kBins;
+    for (int i = threadIdx.x; i < kBins; i += kThreads) stc(&h[i], 0ull);
+  }
+}
+
+__device__ __forceinline__ bool give_up(const Args& a, int row, u32 why) {
+  if (threadIdx.x == 0) a.ctl[row].why = why;
+  return false;
 }
 
 __device__ __forceinline__ void publish_result(const Args& a, int row, long long id, int N, u128 W, u32 kp, u32 idp,
@@ -678,25 +809,37 @@ struct PenTable {
 };
 
 __device__ __forceinline__ void pen_build(const Args& a, int row, int start, int end, PenTable t, Scratch& s) {
-  constexpr int kPer = kMaxHistory / kThreads;  // history ids per thread (registers)
-  const int nw = a.CH >> 5;
+  constexpr int kB = 8;                 // history ids per thread and batch
+  constexpr int kBatch = kB * kThreads;
+  const int nw = kCH >> 5;
   for (int i = threadIdx.x; i < nw; i += kThreads) t.bits[i] = 0u;
   for (int i = threadIdx.x; i < a.seg_cap; i += kThreads) t.cnts[i] = 0u;
-  // the row's history ids that fall in this chunk, chunk-relative (-1 otherwise);
-  // all loads are issued before any is used
+  // the row's history ids in this chunk, chunk-relative (-1 otherwise); the
+  // first batch stays in registers for the counting pass
   const int* h = a.hist + (size_t)row * a.H;
-  int loc[kPer];
+  int loc[kB];
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) {
+  for (int q = 0; q < kB; ++q) {
     const int i = q * kThreads + threadIdx.x;
     loc[q] = i < a.H ? h[i] : -1;
   }
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) loc[q] = (loc[q] >= start && loc[q] < end) ? loc[q] - start : -1;
+  for (int q = 0; q < kB; ++q) loc[q] = (loc[q] >= start && loc[q] < end) ? loc[q] - start : -1;
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < kPer; ++q)
+  for (int q = 0; q < kB; ++q)
     if (loc[q] >= 0) atomicOr(&t.bits[loc[q] >> 5], 1u << (loc[q] & 31));
+  for (int b0 = kBatch; b0 < a.H; b0 += kBatch) {
+    int l2[kB];
+#pragma unroll
+    for (int q = 0; q < kB; ++q) {
+      const int i = b0 + q * kThreads + threadIdx.x;
+      l2[q] = i < a.H ? h[i] : -1;
+    }
+#pragma unroll
+    for (int q = 0; q < kB; ++q)
+      if (l2[q] >= start && l2[q] < end) atomicOr(&t.bits[(l2[q] - start) >> 5], 1u << ((l2[q] - start) & 31));
+  }
   __syncthreads();
   const int per = (nw + kThreads - 1) / kThreads;
   u32 cnt = 0;
@@ -715,11 +858,27 @@ __device__ __forceinline__ void pen_build(const Args& a, int row, int start, int
   }
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) {
+  for (int q = 0; q < kB; ++q) {
     const int l = loc[q];
     if (l >= 0) {
       const u32 bw = t.bits[l >> 5];
       atomicAdd(&t.cnts[t.wpre[l >> 5] + __popc(bw & ((1u << (l & 31)) - 1u))], 1u);
+    }
+  }
+  for (int b0 = kBatch; b0 < a.H; b0 += kBatch) {
+    int l2[kB];
+#pragma unroll
+    for (int q = 0; q < kB; ++q) {
+      const int i = b0 + q * kThreads + threadIdx.x;
+      l2[q] = i < a.H ? h[i] : -1;
+    }
+#pragma unroll
+    for (int q = 0; q < kB; ++q) {
+      if (l2[q] >= start && l2[q] < end) {
+        const int l = l2[q] - start;
+        const u32 bw = t.bits[l >> 5];
+        atomicAdd(&t.cnts[t.wpre[l >> 5] + __popc(bw & ((1u << (l & 31)) - 1u))], 1u);
+      }
     }
   }
   __syncthreads();
@@ -973,261 +1132,773 @@ __device__ __forceinline__ void resolve_single(const Args& a, const RowParams& p
   __syncthreads();
 }
 
-// ---------------------------------------------------------------- top-k finish
+// ---------------------------------------------------------------- chunk loads
 
-// s[0, m): candidates (skey(z) << 32 | ~id), m <= kMergeCap; `zout` is the
-// largest skey(z) of the row's tokens outside them (0 if none).  Resolves
-// top-k, top-p and the draw with LDS radix selects (no sorting); false if the
-// candidates cannot be proven to hold the top-k set.
-__device__ __forceinline__ bool finish_topk(const Args& a, const RowParams& p, int row, u64* s, int m, u32 zout,
-                                            SelLds& L, Scratch& sc) {
-  if (m < p.k) return false;
-  const int tid = threadIdx.x;
-  // key q = z / T
-  for (int i = tid; i < m; i += kThreads) {
-    const u64 c = s[i];
-    s[i] = ((u64)skey(f_of_key((u32)(c >> 32)) / p.T) << 32) | (u32)c;
+// The chunk's logits, 16-byte vectors: thread t holds, for v < NV, the VW
+// logits from start + (v * 256 + t) * VW.  Loads are issued here and consumed
+// by unpack_chunk, so they stay in flight across the penalty table's build.
+template <int DT>
+struct ChunkLoad {
+  static constexpr int VW = (DT == QS_DTYPE_F32) ? 4 : 8;
+  static constexpr int NV = kEPT / VW;
+  static constexpr int ESZ = (DT == QS_DTYPE_F32) ? 4 : 2;
+  uint4 raw[NV];
+  bool vec;
+};
+
+template <int DT>
+__device__ __forceinline__ void issue_chunk(const Args& a, int row, int start, int end, ChunkLoad<DT>& L) {
+  using CL = ChunkLoad<DT>;
+  const char* rp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * CL::ESZ;
+  L.vec = ((((uintptr_t)a.logits) | ((size_t)a.row_stride * CL::ESZ)) & 15) == 0;
+  if (L.vec && end - start == kCH) {
+#pragma unroll
+    for (int v = 0; v < CL::NV; ++v) {
+      const int e0 = start + (v * kThreads + (int)threadIdx.x) * CL::VW;
+      L.raw[v] = *(const uint4*)(rp + (size_t)e0 * CL::ESZ);
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack_chunk(const Args& a, int row, int start, int end, const ChunkLoad<DT>& L,
+                                             float (&z)[kEPT]) {
+  using CL = ChunkLoad<DT>;
+  if (L.vec && end - start == kCH) {
+    // every vector of the chunk was loaded
+#pragma unroll
+    for (int v = 0; v < CL::NV; ++v) {
+      const u32 w4[4] = {L.raw[v].x, L.raw[v].y, L.raw[v].z, L.raw[v].w};
+      if (DT == QS_DTYPE_F32) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) z[v * 4 + j] = __uint_as_float(w4[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          z[v * 8 + 2 * j] = bf16_to_f32(w4[j] & 0xffffu);
+          z[v * 8 + 2 * j + 1] = bf16_to_f32(w4[j] >> 16);
+        }
+      }
+    }
+    return;
+  }
+  // the last chunk of a row, or an unaligned row: element loads
+  const char* rp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * CL::ESZ;
+#pragma unroll
+  for (int v = 0; v < CL::NV; ++v) {
+#pragma unroll
+    for (int j = 0; j < CL::VW; ++j) {
+      const int e = start + (v * kThreads + (int)threadIdx.x) * CL::VW + j;
+      const int ec = e < end ? e : end - 1;
+      const float x = (DT == QS_DTYPE_F32) ? ((const float*)rp)[ec] : bf16_to_f32(((const uint16_t*)rp)[ec]);
+      z[v * CL::VW + j] = e < end ? x : 0.0f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- region writes
+
+// Writes the chunk's tokens whose key kz is at least `thr` to the
+// workgroup's region as (key << 32 | id), in id order: the id start +
+// (v * 256 + t) * VW + j is ordered by (v, t, j).  Returns their number
+// (the same in every thread) and, in *below, the largest key under `thr`.
+// Nothing is written when they do not fit the region.
+template <int DT>
+__device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int start, int end, const u32 (&kz)[kEPT],
+                                           u32 thr, Scratch& sc, u32* below_out) {
+  constexpr int VW = (DT == QS_DTYPE_F32) ? 4 : 8;
+  constexpr int NV = kEPT / VW;
+  constexpr int NW = (NV + 1) / 2;  // counts per vector packed two to a word (16-bit fields)
+  const int tid = threadIdx.x, wv = tid >> 6;
+  if (thr == 0u) thr = 1u;  // key 0 (NaN, or past the end of the row) is never written
+  u32 pk[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) pk[w] = 0u;
+  u32 below = 0u;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      const u32 k = kz[v * VW + j];
+      const bool in = k >= thr;
+      pk[v >> 1] += (in ? 1u : 0u) << (16 * (v & 1));
+      below = (!in && k > below) ? k : below;
+    }
+  }
+  u32 inc[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) inc[w] = wave_incl_scan(pk[w]);
+  const u32 bw = wave_max(below);
+  if (lane_id() == 63) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sc.v[wv][w] = inc[w];
+  }
+  if (lane_id() == 0) sc.v[wv][7] = bw;
+  __syncthreads();
+  u32 base[NW], tot[NW], bmax = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) base[w] = tot[w] = 0u;
+  for (int i = 0; i < kWaves; ++i) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const u32 x = sc.v[i][w];
+      base[w] += (i < wv) ? x : 0u;
+      tot[w] += x;
+    }
+    bmax = sc.v[i][7] > bmax ? sc.v[i][7] : bmax;
   }
   __syncthreads();
-  auto key = [&](int i) { return (u32)(s[i] >> 32); };
-  auto idof = [&](int i) { return 0xffffffffu - (u32)s[i]; };
-  auto all = [&](int) { return true; };
-  auto nowt = [&](int) { return 0ull; };
-  // k-th largest q
-  const SelOut sk = lds_select<false, true>(m, key, all, nowt, (u128)(p.k - 1), L, sc);
-  if (!sk.ok) return false;
-  const u32 kqk = sk.val;
-  QS_TR(6);
-  // every token outside has z <= f_of_key(zout), so q <= that / T: it must be below q_k
-  if (zout > 0u && skey(f_of_key(zout) / p.T) >= kqk) return false;
-  u32 mx = 0u;
-  for (int i = tid; i < m; i += kThreads) mx = key(i) > mx ? key(i) : mx;
-  mx = block_max_u32(mx, sc);
-  const int N = octave_of(f_of_key(mx));
-  auto wt = [&](int i) { return weight_of(f_of_key(key(i)), N); };
-  auto intop = [&](int i) { return key(i) >= kqk; };
+  u32 total = 0u;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) total += (tot[v >> 1] >> (16 * (v & 1))) & 0xffffu;
+  *below_out = bmax;
+  if (total > (u32)a.R) return total;
+  u64* rg = a.cand + ((size_t)row * a.G + blk) * a.R;
+  u32 run = 0u;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int sh = 16 * (v & 1);
+    u32 pos = run + (((base[v >> 1] + inc[v >> 1] - pk[v >> 1]) >> sh) & 0xffffu);
+    const u32 e0 = (u32)(start + (v * kThreads + tid) * VW);
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      const u32 k = kz[v * VW + j];
+      if (k >= thr) {
+        // two 32-bit halves: a 64-bit entry would tie every key to the high
+        // half of a register pair
+        u32* ent = (u32*)&rg[pos];
+        stc(&ent[0], e0 + (u32)j);
+        stc(&ent[1], k);
+        ++pos;
+      }
+    }
+    run += (tot[v >> 1] >> sh) & 0xffffu;
+  }
+  return total;
+}
+
+// ---------------------------------------------------------------- finishing a row from its regions
+
+// Resolves a row from the regions of all its workgroups: the last workgroup of
+// a top-k row (TOPK: entries hold z keys; k-select, then a proof that no token
+// left out could be in the top-k set) or the first workgroup of a peaked mass
+// row (entries hold q keys; `kthr` drops those outside the row's window).
+// The regions are gathered in id order into registers (kFinPer per thread).
+// False if the candidates cannot be proven to hold the answer; the caller then
+// resolves the row with resolve_single.
+template <bool TOPK>
+__device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, int row, u32 kthr, unsigned char* lds,
+                                           Scratch& sc) {
+  const int tid = threadIdx.x;
+  const Slot* sl = a.slots + (size_t)row * a.G;
+  const u64* cd = a.cand + (size_t)row * a.G * a.R;
+  const int total = a.G * a.R;  // <= kRegionTotal, a multiple of kGatherPer
+  const int f0 = tid * kGatherPer;
+  const bool have = f0 < total;
+  const int g = f0 >> a.logR;
+  const u32 s0 = (u32)(f0 & (a.R - 1));
+  // ---- gather: this thread's kGatherPer region entries and their region's header
+  u64 ent[kGatherPer];
+  u32 cnt = 0u, tau = 0u, below = 0u;
+  if (have) {
+    cnt = ldc(&sl[g].nb);
+    if (TOPK) {
+      tau = ldc(&sl[g].tau);
+      below = ldc(&sl[g].below);
+    }
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q) ent[q] = ldc(&cd[f0 + q]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q) ent[q] = 0ull;
+  }
+  u32 ovf = (have && cnt == 0xffffffffu) ? 1u : 0u;
+  u32 tstar = tau;
+  block_max3(tstar, ovf, below, sc);
+  QS_TR(11);
+  if (ovf) return give_up(a, row, kWhyRegion);
+  // ---- entries at or above the threshold, compacted in id order through LDS
+  const u32 thr = TOPK ? tstar : kthr;
+  u32 flags = 0u, npass = 0u, dropmax = 0u;
+#pragma unroll
+  for (int q = 0; q < kGatherPer; ++q) {
+    if (have && s0 + (u32)q < cnt) {
+      const u32 k = (u32)(ent[q] >> 32);
+      if (k >= thr) {
+        flags |= 1u << q;
+        ++npass;
+      } else {
+        dropmax = k > dropmax ? k : dropmax;
+      }
+    }
+  }
+  u32 m;
+  const u32 off = block_scan_u32(npass, sc, &m);
+  u32 nout = 0u;
+  if (TOPK) nout = block_max_u32(dropmax > below ? dropmax : below, sc);
+  if (m > (u32)kFinCap) return give_up(a, row, kWhyMerge);
+  if (TOPK && m < (u32)p.k) return give_up(a, row, kWhyFewer);
+  u64* stage = (u64*)lds;
+  {
+    u32 pos = off;
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q)
+      if ((flags >> q) & 1u) stage[pos++] = ent[q];
+  }
+  __syncthreads();
+  u32 key[kFinPer], id[kFinPer], wp[kFinPer], memb = 0u;
+#pragma unroll
+  for (int j = 0; j < kFinPer; ++j) {
+    const u32 i = (u32)(tid * kFinPer + j);
+    if (i < m) {
+      const u64 e = stage[i];
+      key[j] = (u32)(e >> 32);
+      id[j] = (u32)e;
+      memb |= 1u << j;
+    } else {
+      key[j] = 0u;
+      id[j] = 0u;
+    }
+  }
+  __syncthreads();  // the staging area becomes the select buffers
+  QS_TR(5);
+  // ---- q keys, the row scale, packed weights
+  u32 kmx = 0u;
+#pragma unroll
+  for (int j = 0; j < kFinPer; ++j) {
+    if ((memb >> j) & 1u) {
+      if (TOPK) key[j] = skey(f_of_key(key[j]) / p.T);
+      kmx = key[j] > kmx ? key[j] : kmx;
+    }
+  }
+  kmx = block_max_u32(kmx, sc);
+  const int N = octave_of(f_of_key(kmx));
+#pragma unroll
+  for (int j = 0; j < kFinPer; ++j) wp[j] = ((memb >> j) & 1u) ? wpack(f_of_key(key[j]), N) : 0u;
+  SelLds* SL = (SelLds*)lds;
+  // ---- top-k: the k-th largest q, and the proof that the candidates hold the top-k set
+  u32 kappa = 0u;
+  if (TOPK) {
+    const SelOut sk = reg_select<false>(key, memb, wp, (u128)(p.k - 1), SL, sc);
+    if (!sk.ok) return give_up(a, row, kWhyKSelect);
+    kappa = sk.val;
+    QS_TR(6);
+    // every token left out has z <= f_of_key(nout), so q <= that / T: it must be below the k-th
+    if (nout > 0u && skey(f_of_key(nout) / p.T) >= kappa) return give_up(a, row, kWhyIncomplete);
+  }
+  u32 intop = 0u;
   u128 sv = 0;
-  for (int i = tid; i < m; i += kThreads)
-    if (intop(i)) sv += (u128)wt(i);
+#pragma unroll
+  for (int j = 0; j < kFinPer; ++j) {
+    if (((memb >> j) & 1u) && key[j] >= kappa) {
+      intop |= 1u << j;
+      sv += (u128)wunpack(wp[j]);
+    }
+  }
   const u128 S = block_sum128(sv, sc);
   QS_TR(13);
-  u32 kappa_p = kqk, id_p = 0xffffffffu;  // kept: key > kappa_p || (key == kappa_p && id <= id_p)
+  u32 kp = kappa, idp = 0xffffffffu;  // kept: key > kp || (key == kp && id <= idp)
   u128 W = S;
   if (p.topp_on) {
     // the first token (q desc, id asc) whose inclusive mass exceeds floor(top_p * S)
     const u128 Tp = mul_frac(S, p.tp);
-    const SelOut sp = lds_select<true, true>(m, key, intop, wt, Tp, L, sc);
+    const SelOut sp = reg_select<true>(key, intop, wp, Tp, SL, sc);
     QS_TR(14);
-    if (!sp.ok) return false;
-    kappa_p = sp.val;
+    if (!sp.ok) return give_up(a, row, kWhyTopP);
+    kp = sp.val;
     const u128 A = acc_mass(sp.before);
-    const u64 wk = weight_of(f_of_key(kappa_p), N);
-    const u64 j = div_small(Tp - A, wk);  // 0-based boundary member among the ties (< sp.at.c)
-    if (j + 1 >= sp.at.c) {
+    const u64 wk = wunpack(wpack(f_of_key(kp), N));
+    const u64 jb = div_small(Tp - A, wk);  // 0-based boundary member among the ties (< sp.at.c)
+    if (jb + 1 >= sp.at.c) {
       W = A + acc_mass(sp.at);
     } else {
-      W = A + (u128)wk * (u128)(j + 1);
-      auto intie = [&](int i) { return key(i) == kappa_p; };
-      const SelOut si = lds_select<false, false>(m, idof, intie, nowt, (u128)j, L, sc);
-      if (!si.ok) return false;
-      id_p = si.val;
+      W = A + (u128)wk * (u128)(jb + 1);
+      // the boundary member: tie member jb in id order, which is register order
+      u32 c = 0u;
+#pragma unroll
+      for (int j = 0; j < kFinPer; ++j) c += (((intop >> j) & 1u) && key[j] == kp) ? 1u : 0u;
+      if (tid == 0) sc.r[5] = 0xffffffffu;
+      u32 ct;
+      const u32 ex = block_scan_u32(c, sc, &ct);
+      if (jb >= ex && jb < (u64)ex + c) {
+        u32 r = ex;
+#pragma unroll
+        for (int j = 0; j < kFinPer; ++j) {
+          if (((intop >> j) & 1u) && key[j] == kp) {
+            if (r == (u32)jb) sc.r[5] = id[j];
+            ++r;
+          }
+        }
+      }
+      __syncthreads();
+      idp = sc.r[5];
+      __syncthreads();
     }
   }
-  // draw: kept tokens in ascending id, the first whose inclusive mass exceeds floor(u * W)
+  QS_TR(7);
+  // ---- the draw: kept tokens in id order (register order), the first whose
+  // inclusive mass exceeds floor(u * W)
   const u128 t = mul_frac(W, p.u);
-  auto kept = [&](int i) {
-    const u32 k = key(i);
-    return k > kappa_p || (k == kappa_p && idof(i) <= id_p);
-  };
-  const SelOut sd = lds_select<true, false>(m, idof, kept, wt, t, L, sc);
+  u32 keptm = 0u;
+  u128 mine = 0;
+#pragma unroll
+  for (int j = 0; j < kFinPer; ++j) {
+    if (((memb >> j) & 1u) && (key[j] > kp || (key[j] == kp && id[j] <= idp))) {
+      keptm |= 1u << j;
+      mine += (u128)wunpack(wp[j]);
+    }
+  }
+  if (tid == 0) sc.r[6] = 0xffffffffu;
+  Acc tot;
+  const Acc ex = block_scan_acc(acc_of(mine, 0u), sc, &tot);
+  {
+    const u128 lo = acc_mass(ex);
+    if (t >= lo && t < lo + mine) {
+      u128 run = lo;
+      bool found = false;
+#pragma unroll
+      for (int j = 0; j < kFinPer; ++j) {
+        if (!found && ((keptm >> j) & 1u)) {
+          run += (u128)wunpack(wp[j]);
+          if (run > t) {
+            sc.r[6] = id[j];
+            found = true;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const u32 chosen = sc.r[6];
+  __syncthreads();
+  QS_TR(9);
   if (tid == 0)
-    publish_result(a, row, sd.ok ? (long long)sd.val : -1ll, N, W, kappa_p, id_p, false, 1u);
+    publish_result(a, row, chosen == 0xffffffffu ? -1ll : (long long)chosen, N, W, kp, idp, false, TOPK ? 1u : 4u);
   __syncthreads();
   return true;
 }
 
-// ---------------------------------------------------------------- mass rows
-
-
-struct MassLds {
-  u64 h[kBins];             // local histogram (fixed-point mass >> 24)
-  u64 g[kBins];             // merged histogram, read back
-  u64 a_lo[kMaxChunks];     // per-chunk published mass (chunk mass or mass above the bracket)
-  u64 a_hi[kMaxChunks];
-  u32 nbv[kMaxChunks];      // per-chunk bracketed token count
-  u32 pref[kMaxChunks];     // exclusive prefix of nbv
-  u64 c_lo[kMaxChunks];     // per-chunk kept mass of bracketed tokens, lo 32-bit parts
-  u64 c_hi[kMaxChunks];     //   hi parts
-  u64 list[kBracketCap];    // bracketed tokens (key << 32 | ~id)
-  SelLds sel;
-};
-
-__device__ __forceinline__ void load_slots(MassLds& M, const Slot* sl, int G) {
-  for (int g = threadIdx.x; g < G; g += kThreads) {
-    M.a_lo[g] = ldc(&sl[g].s_lo);
-    M.a_hi[g] = ldc(&sl[g].s_hi);
-    M.nbv[g] = ldc(&sl[g].nb);
-  }
-  __syncthreads();
-}
+// ---------------------------------------------------------------- flat mass rows
 
 // Bracket of bins [blo, bhi] that provably holds the top-p boundary (the first
-// token, in descending order, whose inclusive mass exceeds Tp).  `g` holds,
-// per bin, the sum over its tokens of (w >> 24); `above` is the same-units
-// mass above the histogram's range and `err` bounds the truncation over all
-// tokens counted (each loses less than one unit).  One bin per thread.
+// token, in descending order, whose inclusive mass exceeds Tp).  g[b] is the
+// sum over bin b's tokens of (w >> shift); each token truncates less than one
+// unit, so `err` (the number of tokens) bounds the error of any sum of bins.
+// One bin per thread.
 //   bhi: the lowest bin whose mass above it is provably <= Tp;
 //   blo: the highest bin whose mass at or above it is provably > Tp.
-__device__ __forceinline__ void bracket_bins(const u64* g, u64 above, u64 err, u128 Tp, Scratch& sc, int* blo,
+__device__ __forceinline__ void bracket_bins(const u64* g, u64 err, u128 Tp, int shift, Scratch& sc, int* blo,
                                              int* bhi) {
   static_assert(kBins == kThreads, "one histogram bin per thread");
   const int tid = threadIdx.x;
   const int b = kBins - 1 - tid;  // thread order = descending bins
   const u64 gb = g[b];
+  if (tid == 0) {
+    sc.r[10] = 0xffffffffu;  // min over bins meeting the bhi condition
+    sc.r[11] = 0u;           // max over bins meeting the blo condition, +1
+  }
   Acc tot;
   const Acc ex = block_scan_acc(acc_of((u128)gb, 0u), sc, &tot);
-  const u128 run = (u128)above + acc_mass(ex);  // lower bound of the mass above bin b
-  if (tid == 0) {
-    sc.r[6] = 0xffffffffu;  // min over bins satisfying the bhi condition
-    sc.r[7] = 0u;           // max over bins satisfying the blo condition, +1
-  }
+  const u128 run = acc_mass(ex);  // lower bound of the mass above bin b, in units
+  if (((run + err) << shift) <= Tp) atomicMin(&sc.r[10], (u32)b);
+  if (((run + gb) << shift) > Tp) atomicMax(&sc.r[11], (u32)b + 1u);
   __syncthreads();
-  if (((run + err) << 24) <= Tp) atomicMin(&sc.r[6], (u32)b);
-  if (((run + gb) << 24) > Tp) atomicMax(&sc.r[7], (u32)b + 1u);
-  __syncthreads();
-  int hi = sc.r[6] == 0xffffffffu ? kBins - 1 : (int)sc.r[6];
-  int lo = sc.r[7] == 0u ? 0 : (int)sc.r[7] - 1;
+  int hi = sc.r[10] == 0xffffffffu ? kBins - 1 : (int)sc.r[10];
+  int lo = sc.r[11] == 0u ? 0 : (int)sc.r[11] - 1;
   __syncthreads();
   if (lo > hi) lo = hi;
   *blo = lo;
   *bhi = hi;
 }
 
-// ---------------------------------------------------------------- main kernel
+// The histogram bin of y in a flat mass row.
+__device__ __forceinline__ int mass_bin(double y, double ylo, double bscale) {
+  const int b = (int)((y - ylo) * bscale);
+  return b < 0 ? 0 : (b > kBins - 1 ? kBins - 1 : b);
+}
 
-// ROLE 0 resolves greedy, top-k and large-k rows (and mass rows when no mass
-// launch follows); ROLE 1 resolves the mass rows only.
-template <int DT, int EPT, int ROLE>
-__global__ __launch_bounds__(kThreads) void k_sample(Args a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  __shared__ Scratch sc;
-  __shared__ u32 tmax_s[kThreads];
-  constexpr int VW = (DT == QS_DTYPE_F32) ? 4 : 8;
-  constexpr int NV = EPT / VW;
-  const int row = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
-  const int start = blk * a.CH;
-  const int end = min(a.V, start + a.CH);
-  const RowParams p = row_params(a, row);
-  RowCtl* c = a.ctl + row;
-  if (ROLE == 1 && p.kind != kMass) return;
-  if (ROLE == 0 && p.kind == kMass && !(a.flags & QS_FLAG_NO_MASS_ROWS)) return;
-  QS_TR(0);
-
-  if (ROLE == 0 && (p.kind == kSingle || p.kind == kMass)) {
-    if (blk == 0) {
-      if (DT == QS_DTYPE_F32) resolve_single<QS_DTYPE_F32>(a, p, row, lds, sc);
-      else resolve_single<QS_DTYPE_BF16>(a, p, row, lds, sc);
-    }
-    if (arrive_last(c, (u32)a.G, sc)) reset_row(a, row);
-    return;
-  }
-
-  // ---- penalty table for the chunk, then the chunk into registers
+// Locates the drawn token inside chunk g: kept tokens (key > kp || (key == kp
+// && id <= idp)) in id order, the first whose inclusive mass within the chunk
+// exceeds tl.  Re-reads the chunk; thread t takes the kEPT tokens from
+// start + t * kEPT.  Returns the id (0xffffffff if none).
+template <int DT>
+__device__ __forceinline__ u32 draw_in_chunk(const Args& a, const RowParams& p, int row, int g, int N, u32 kp, u32 idp,
+                                             u128 tl, unsigned char* lds, Scratch& sc) {
+  const int tid = threadIdx.x;
+  const int start = g * kCH, end = min(a.V, start + kCH);
   PenTable pt;
   pt.bits = (u32*)lds;
-  pt.wpre = pt.bits + (a.CH >> 5);
-  pt.cnts = pt.wpre + (a.CH >> 5);
-  if (p.pen_on) pen_build(a, row, start, end, pt, sc);
-  QS_TR(1);
-
-  float z[EPT];
+  pt.wpre = pt.bits + (kCH >> 5);
+  pt.cnts = pt.wpre + (kCH >> 5);
+  const int e0 = start + tid * kEPT;
+  float z[kEPT];
   {
-    const bool vec = ((((uintptr_t)a.logits) | ((size_t)a.row_stride * (DT == QS_DTYPE_F32 ? 4 : 2))) & 15) == 0;
+    constexpr int ESZ = (DT == QS_DTYPE_F32) ? 4 : 2;
+    constexpr int VW = 16 / ESZ;
+    const char* rp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * ESZ;
+    const bool vec = ((((uintptr_t)a.logits) | ((size_t)a.row_stride * ESZ)) & 15) == 0;
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int e0 = start + (v * kThreads + tid) * VW;
-      if (vec && e0 + VW <= end) {
+    for (int v = 0; v < kEPT / VW; ++v) {
+      const int ev = e0 + v * VW;
+      if (vec && ev + VW <= end) {
+        const uint4 r = *(const uint4*)(rp + (size_t)ev * ESZ);
+        const u32 w4[4] = {r.x, r.y, r.z, r.w};
         if (DT == QS_DTYPE_F32) {
-          const float4 q = *(const float4*)((const float*)a.logits + (size_t)row * a.row_stride + e0);
-          z[v * VW + 0] = q.x;
-          z[v * VW + 1] = q.y;
-          z[v * VW + 2] = q.z;
-          z[v * VW + 3] = q.w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) z[v * 4 + j] = __uint_as_float(w4[j]);
         } else {
-          const uint4 q = *(const uint4*)((const uint16_t*)a.logits + (size_t)row * a.row_stride + e0);
-          const u32 w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            z[v * VW + 2 * j] = bf16_to_f32(w4[j] & 0xffffu);
-            z[v * VW + 2 * j + 1] = bf16_to_f32(w4[j] >> 16);
+            z[v * 8 + 2 * j] = bf16_to_f32(w4[j] & 0xffffu);
+            z[v * 8 + 2 * j + 1] = bf16_to_f32(w4[j] >> 16);
           }
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          const int e = e0 + j;
-          z[v * VW + j] = (e < end) ? load_logit<DT>(a, row, e) : 0.0f;
-        }
+        for (int j = 0; j < VW; ++j) z[v * VW + j] = (ev + j < end) ? load_logit<DT>(a, row, ev + j) : 0.0f;
       }
-      if (p.pen_on) {
+    }
+  }
+  if (p.pen_on) pen_build(a, row, start, end, pt, sc);
+  u128 mine = 0;
 #pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          const int e = e0 + j;
-          if (e < end) {
-            const u32 cnt = pen_count(pt, e - start);
-            if (cnt) z[v * VW + j] = apply_penalty(z[v * VW + j], cnt, p.rep, p.pres, p.freq);
+  for (int j = 0; j < kEPT; ++j) {
+    const int e = e0 + j;
+    if (e < end) {
+      float zz = z[j];
+      if (p.pen_on) {
+        const u32 cnt = pen_count(pt, e - start);
+        if (cnt) zz = apply_penalty(zz, cnt, p.rep, p.pres, p.freq);
+      }
+      const float q = zz / p.T;
+      z[j] = q;
+      const u32 k = skey(q);
+      if (k > kp || (k == kp && (u32)e <= idp)) mine += (u128)weight_of(q, N);
+    }
+  }
+  if (tid == 0) sc.r[9] = 0xffffffffu;
+  Acc tot;
+  const Acc ex = block_scan_acc(acc_of(mine, 0u), sc, &tot);
+  {
+    const u128 lo = acc_mass(ex);
+    if (tl >= lo && tl < lo + mine) {
+      u128 run = lo;
+      bool found = false;
+#pragma unroll
+      for (int j = 0; j < kEPT; ++j) {
+        const int e = e0 + j;
+        if (!found && e < end) {
+          const u32 k = skey(z[j]);
+          if (k > kp || (k == kp && (u32)e <= idp)) {
+            run += (u128)weight_of(z[j], N);
+            if (run > tl) {
+              sc.r[9] = (u32)e;
+              found = true;
+            }
           }
         }
       }
     }
   }
-  if (p.pen_on) __syncthreads();  // the LDS table is reused below
+  __syncthreads();
+  const u32 id = sc.r[9];
+  __syncthreads();
+  return id;
+}
 
-#define QS_FOR_ELEMS(...)                                   \
-  _Pragma("unroll") for (int v = 0; v < NV; ++v) {          \
-    _Pragma("unroll") for (int j = 0; j < VW; ++j) {        \
-      const int e = start + (v * kThreads + tid) * VW + j;  \
-      if (e < end) {                                        \
-        float& zz = z[v * VW + j];                          \
-        (void)zz;                                           \
-        __VA_ARGS__                                         \
-      }                                                     \
-    }                                                       \
+// The id of the member of rank `rank` (0-based, id order) among the tokens of
+// chunk g whose key is kp.  Re-reads the chunk like draw_in_chunk.
+template <int DT>
+__device__ __forceinline__ u32 rank_in_chunk(const Args& a, const RowParams& p, int row, int g, u32 kp, u32 rank,
+                                             unsigned char* lds, Scratch& sc) {
+  const int tid = threadIdx.x;
+  const int start = g * kCH, end = min(a.V, start + kCH);
+  PenTable pt;
+  pt.bits = (u32*)lds;
+  pt.wpre = pt.bits + (kCH >> 5);
+  pt.cnts = pt.wpre + (kCH >> 5);
+  if (p.pen_on) pen_build(a, row, start, end, pt, sc);
+  const int e0 = start + tid * kEPT;
+  u32 mk = 0u, c = 0u;  // bit j: token e0 + j has key kp
+#pragma unroll
+  for (int j = 0; j < kEPT; ++j) {
+    const int e = e0 + j;
+    if (e < end) {
+      float zz = load_logit<DT>(a, row, e);
+      if (p.pen_on) {
+        const u32 cnt = pen_count(pt, e - start);
+        if (cnt) zz = apply_penalty(zz, cnt, p.rep, p.pres, p.freq);
+      }
+      if (skey(zz / p.T) == kp) {
+        mk |= 1u << j;
+        ++c;
+      }
+    }
   }
+  if (tid == 0) sc.r[9] = 0xffffffffu;
+  u32 ct;
+  const u32 ex = block_scan_u32(c, sc, &ct);
+  if (rank >= ex && rank < ex + c) {
+    u32 r = ex;
+#pragma unroll
+    for (int j = 0; j < kEPT; ++j) {
+      if ((mk >> j) & 1u) {
+        if (r == rank) sc.r[9] = (u32)(e0 + j);
+        ++r;
+      }
+    }
+  }
+  __syncthreads();
+  const u32 id = sc.r[9];
+  __syncthreads();
+  return id;
+}
+
+// LDS of the flat-row resolver: two select buffers; per chunk, the kept mass
+// of its bracket entries above the boundary key and its count of tokens at it.
+struct FlatLds {
+  SelLds sel[2];
+  u64 clo[kMaxChunks];
+  u64 chi[kMaxChunks];
+  u32 ckp[kMaxChunks];
+};
+
+// A flat mass row after k_sample: the top-p boundary from the bracket entries
+// (topp) or none, the kept mass per chunk, the chunk holding the draw target,
+// and the token inside it.  With `topp` false every token is kept and the
+// chunk masses are the slots' s values.
+template <int DT>
+__device__ __forceinline__ bool resolve_flat(const Args& a, const RowParams& p, int row, int N, bool topp, u128 Tp,
+                                             bool bottom, unsigned char* lds, Scratch& sc) {
+  const int tid = threadIdx.x;
+  const Slot* sl = a.slots + (size_t)row * a.G;
+  RowCtl* c = a.ctl + row;
+  FlatLds& F = *(FlatLds*)lds;
+  // per-chunk mass above the bracket (topp) or of the whole chunk
+  u128 ag = 0;
+  if (tid < a.G) ag = topp ? mk128(ldc(&sl[tid].a_lo), ldc(&sl[tid].a_hi)) : mk128(ldc(&sl[tid].s_lo), ldc(&sl[tid].s_hi));
+  u32 kp = 0u, idp = 0xffffffffu;  // kept: key > kp || (key == kp && id <= idp)
+  u64 wk = 0ull;                   // weight of a token at kp
+  u32 J = 0u;                      // tokens at kp kept (in id order), if they are split
+  bool split = false;
+  if (tid < kMaxChunks) {
+    F.clo[tid] = 0ull;
+    F.chi[tid] = 0ull;
+    F.ckp[tid] = 0u;
+  }
+  if (topp) {
+    const u32 m = ldc(&c->list_n);
+    const u32 st = ldc(&c->status);
+    const u64* lst = a.list + (size_t)row * kListCap;
+    u32 key[kFinPer], cnt[kFinPer], wp[kFinPer], memb = 0u;
+    int ch[kFinPer];
+#pragma unroll
+    for (int j = 0; j < kFinPer; ++j) {
+      const u32 i = (u32)(tid * kFinPer + j);
+      const bool in = i < m && i < (u32)kListCap;
+      const u64 e = in ? ldc(&lst[i]) : 0ull;
+      key[j] = (u32)(e >> 32);
+      cnt[j] = (u32)e & 0xffffu;
+      ch[j] = (int)(((u32)e >> 16) & 0xffu);
+      if (in) memb |= 1u << j;
+    }
+    const u128 A = block_sum128(ag, sc);
+    QS_TR(1);
+    if (m > (u32)kListCap || (st & kStList)) return give_up(a, row, kWhyList);
+    if (A > Tp) return give_up(a, row, kWhyAbove);
+#pragma unroll
+    for (int j = 0; j < kFinPer; ++j) wp[j] = ((memb >> j) & 1u) ? wpack(f_of_key(key[j]), N) : 0u;
+    const SelOut sp = reg_select<true, kFinPer, true>(key, memb, wp, Tp - A, F.sel, sc, cnt);
+    QS_TR(2);
+    if (!sp.ok) {
+      // every bracketed token is kept: right only if nothing with weight lies below
+      if (!bottom) return give_up(a, row, kWhyBracket);
+    } else {
+      kp = sp.val;
+      const u128 A2 = A + acc_mass(sp.before);
+      wk = wunpack(wpack(f_of_key(kp), N));
+      const u64 jb = div_small(Tp - A2, wk);  // 0-based boundary member among the tokens at kp
+      if (jb + 1 < sp.at.c) {
+        split = true;
+        J = (u32)jb + 1u;
+      }
+    }
+    // per chunk: mass of the entries above kp, tokens at kp
+#pragma unroll
+    for (int j = 0; j < kFinPer; ++j) {
+      if ((memb >> j) & 1u) {
+        if (key[j] > kp) {
+          const u64 w = wunpack(wp[j]);
+          atomicAdd(&F.clo[ch[j]], (w & 0xffffffffull) * cnt[j]);
+          atomicAdd(&F.chi[ch[j]], (w >> 32) * cnt[j]);
+        } else if (key[j] == kp) {
+          atomicAdd(&F.ckp[ch[j]], cnt[j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // kept mass per chunk (one chunk per thread); tokens at kp are kept in id
+  // order, chunk by chunk, until J of them
+  u32 kpc = (tid < a.G) ? F.ckp[tid] : 0u;
+  u32 kpt;
+  const u32 kpre = block_scan_u32(kpc, sc, &kpt);
+  u32 keep = kpc;
+  if (split) keep = J > kpre ? min(kpc, J - kpre) : 0u;
+  if (tid == 0) {
+    sc.r[8] = 0xffffffffu;
+    sc.r[14] = 0xffffffffu;
+  }
+  u128 kg = 0;
+  if (tid < a.G) kg = ag + mk128(F.clo[tid], 0) + ((u128)F.chi[tid] << 32) + (u128)wk * keep;
+  Acc tot;
+  const Acc ex = block_scan_acc(acc_of(kg, 0u), sc, &tot);  // its barriers order the writes below after the ones above
+  // the chunk holding the boundary token (the J-th at kp) and its rank there
+  if (split && tid < a.G && J - 1u >= kpre && J - 1u < kpre + kpc) {
+    sc.r[14] = (u32)tid;
+    sc.r[15] = J - 1u - kpre;
+  }
+  const u128 W = acc_mass(tot);
+  const u128 t = mul_frac(W, p.u);
+  if (tid < a.G && t >= acc_mass(ex) && t < acc_mass(ex) + kg) {
+    sc.r[8] = (u32)tid;
+    const u128 tl = t - acc_mass(ex);
+    sc.w[16] = (u64)tl;
+    sc.w[17] = (u64)(tl >> 64);
+  }
+  __syncthreads();
+  const u32 owner = sc.r[8];
+  const u128 tl = mk128(sc.w[16], sc.w[17]);
+  const u32 gb = sc.r[14], rb = sc.r[15];
+  __syncthreads();
+  QS_TR(3);
+  if (owner == 0xffffffffu) return give_up(a, row, kWhyOwner);
+  if (split) {
+    if (gb == 0xffffffffu) return give_up(a, row, kWhyTie);
+    idp = rank_in_chunk<DT>(a, p, row, (int)gb, kp, rb, lds, sc);
+    if (idp == 0xffffffffu) return give_up(a, row, kWhyTie);
+  }
+  QS_TR(8);
+  const u32 chosen = draw_in_chunk<DT>(a, p, row, (int)owner, N, kp, idp, tl, lds, sc);
+  QS_TR(10);
+  if (tid == 0)
+    publish_result(a, row, chosen == 0xffffffffu ? -1ll : (long long)chosen, N, W, kp, idp, false, 2u);
+  __syncthreads();
+  return true;
+}
+
+// The chunk of a row into registers, history penalties applied: thread t
+// holds z[v * VW + j] = logit start + (v * 256 + t) * VW + j.
+template <int DT>
+__device__ __forceinline__ void load_chunk_pen(const Args& a, const RowParams& p, int row, int start, int end,
+                                               float (&z)[kEPT], unsigned char* lds, Scratch& sc) {
+  constexpr int VW = ChunkLoad<DT>::VW;
+  constexpr int NV = ChunkLoad<DT>::NV;
+  const int tid = threadIdx.x;
+  PenTable pt;
+  pt.bits = (u32*)lds;
+  pt.wpre = pt.bits + (kCH >> 5);
+  pt.cnts = pt.wpre + (kCH >> 5);
+  ChunkLoad<DT> cl;
+  // bf16: the loads overlap the table's build; fp32 chunks are twice the
+  // registers, so they are loaded after it
+  if (DT == QS_DTYPE_BF16) issue_chunk<DT>(a, row, start, end, cl);
+  if (p.pen_on) pen_build(a, row, start, end, pt, sc);
+  if (DT == QS_DTYPE_F32) issue_chunk<DT>(a, row, start, end, cl);
+  unpack_chunk<DT>(a, row, start, end, cl, z);
+  if (p.pen_on) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        const int e = start + (v * kThreads + tid) * VW + j;
+        if (e < end) {
+          const u32 cnt = pen_count(pt, e - start);
+          if (cnt) z[v * VW + j] = apply_penalty(z[v * VW + j], cnt, p.rep, p.pres, p.freq);
+        }
+      }
+    }
+    __syncthreads();  // the LDS table is reused after
+  }
+}
+
+// ---------------------------------------------------------------- streaming kernel
+
+// One workgroup per (chunk, row).  ROLE 0: greedy rows (resolved here by the
+// last workgroup to arrive) and the regions of top-k rows; ROLE 1: mass rows
+// (regions, the row maximum, and for flat rows the bin masses, the bracket and
+// the bracketed tokens).  k_finish resolves the other rows afterwards.
+template <int DT, int ROLE>
+__global__ __launch_bounds__(kThreads) void k_sample(Args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  __shared__ Scratch sc;
+  constexpr int VW = ChunkLoad<DT>::VW;
+  constexpr int NV = ChunkLoad<DT>::NV;
+  const int row = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int start = blk * kCH;
+  const int end = min(a.V, start + kCH);
+  const RowParams p = row_params(a, row);
+  RowCtl* c = a.ctl + row;
+  if (ROLE == 1 && p.kind != kMass) return;
+  if (ROLE == 0 && (p.kind == kMass || p.kind == kSingle)) return;
+#ifdef QS_TRACE
+  if (tid == 0) sc.tslot = (u32)(row * a.G + blk);
+#endif
+  QS_TR(0);
+
+  // token (v, j) of this thread is start + (v * 256 + tid) * VW + j, inside the
+  // row iff j < lim[v]
+  int lim[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) lim[v] = (end - start) - (v * kThreads + tid) * VW;
 
   if constexpr (ROLE == 0) {
-  // ================================================================ greedy
-  if (p.kind == kGreedy) {
-    u64 best = 0ull;
-    QS_FOR_ELEMS({
-      const u64 pk = ((u64)gkey(zz) << 32) | (0xffffffffu - (u32)e);
-      best = pk > best ? pk : best;
-    })
-    best = block_max_u64(best, sc);
-    QS_TR(2);
-    if (tid == 0) maxc(&c->pack, best);
-    if (arrive_last(c, (u32)a.G, sc)) {
-      QS_TR(4);
-      if (tid == 0) {
-        const u64 pk = maxc(&c->pack, 0ull);
-        publish_result(a, row, (long long)(0xffffffffu - (u32)pk), 0, 0, 0u, 0u, true, 0u);
+    // ================================================================ greedy
+    if (p.kind == kGreedy) {
+      float z[kEPT];
+      load_chunk_pen<DT>(a, p, row, start, end, z, lds, sc);
+      QS_TR(1);
+      // this thread's tokens in increasing id: the first of the largest keys
+      u32 bk = 0u;
+      int bi = -1;
+#pragma unroll
+      for (int i = 0; i < kEPT; ++i) {
+        const u32 gk = gkey(z[i]);
+        const bool take = (i % VW) < lim[i / VW] && (bi < 0 || gk > bk);
+        bk = take ? gk : bk;
+        bi = take ? i : bi;
       }
-      reset_row(a, row);
+      const u32 be = (u32)(start + ((bi / VW) * kThreads + tid) * VW + (bi % VW));
+      u64 best = bi < 0 ? 0ull : (((u64)bk << 32) | (0xffffffffu - be));
+      best = block_max_u64(best, sc);
+      QS_TR(2);
+      if (tid == 0) maxc(&c->pack, best);
+      if (arrive_last(c, (u32)a.G, sc)) {
+        QS_TR(4);
+        if (tid == 0) {
+          const u64 pk = maxc(&c->pack, 0ull);
+          publish_result(a, row, (long long)(0xffffffffu - (u32)pk), 0, 0, 0u, 0u, true, 0u);
+        }
+        reset_row(a, row);
+      }
+      return;
     }
-    return;
-  }
 
-  // ================================================================ top-k
-  if (p.kind == kTopK) {
-    u32 tm = 0u;
-    QS_FOR_ELEMS({
-      const u32 k = skey(zz);
-      tm = k > tm ? k : tm;
-    })
-    // tau: at least kc tokens of the chunk are >= tau.  kc covers this chunk's
+    // ================================================================ top-k
+    // tau: at least kc tokens of the chunk are >= tau, kc covering this chunk's
     // expected share of the row's top-k with a wide margin.  Each wave sorts
     // its 64 per-thread maxima (shuffles) and takes the ceil(kc/4)-th largest;
     // the workgroup takes the smallest of the four.
+    float z[kEPT];
+    load_chunk_pen<DT>(a, p, row, start, end, z, lds, sc);
+    QS_TR(1);
+    u32 kz[kEPT];
+    u32 tm = 0u;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      kz[i] = ((i % VW) < lim[i / VW]) ? skey(z[i]) : 0u;
+      tm = kz[i] > tm ? kz[i] : tm;
+    }
     const float mu = (float)p.k / (float)a.G;
     int kc = (int)ceilf(mu) + 4 * (int)ceilf(sqrtf(mu)) + 4;
     kc = min(kc, min(p.k, kThreads));
@@ -1242,611 +1913,238 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
       }
     }
     const u32 tw = __shfl(x, kw - 1, 64);
-    if (lane == 0) tmax_s[tid >> 6] = tw;
+    if (lane == 0) sc.v[tid >> 6][6] = tw;
     __syncthreads();
     QS_TR(2);
-    u32 tau = tmax_s[0];
-    for (int w = 1; w < kWaves; ++w) tau = tmax_s[w] < tau ? tmax_s[w] : tau;
-    u32 mine = 0, below = 0u;
-    QS_FOR_ELEMS({
-      const u32 k = skey(zz);
-      if (k >= tau) ++mine;
-      else below = k > below ? k : below;
-    })
-    below = block_max_u32(below, sc);
-    u32 total;
-    const u32 off = block_scan_u32(mine, sc, &total);
-    const bool fits = total <= (u32)kBlockCand;
-    if (fits) {
-      u64* cd = a.cand + ((size_t)row * a.G + blk) * kBlockCand + off;
-      u32 pos = 0;
-      QS_FOR_ELEMS({
-        const u32 k = skey(zz);
-        if (k >= tau) {
-          stc(&cd[pos], ((u64)k << 32) | (0xffffffffu - (u32)e));
-          ++pos;
-        }
-      })
-    }
-    Slot* sl = a.slots + (size_t)row * a.G + blk;
+    u32 tau = sc.v[0][6];
+    for (int w = 1; w < kWaves; ++w) tau = sc.v[w][6] < tau ? sc.v[w][6] : tau;
+    u32 below;
+    const u32 total = emit_region<DT>(a, row, blk, start, end, kz, tau, sc, &below);
     if (tid == 0) {
-      stc(&sl->nb, fits ? total : 0xffffffffu);
-      stc(&sl->pad[0], tau);
-      stc(&sl->pad[1], below);
+      Slot* sl = a.slots + (size_t)row * a.G + blk;
+      stc(&sl->nb, total <= (u32)a.R ? total : 0xffffffffu);
+      stc(&sl->tau, tau);
+      stc(&sl->below, below);
     }
     QS_TR(3);
-    if (!arrive_last(c, (u32)a.G, sc)) {
-      QS_TR(15);
-      return;
+    return;
+  } else {
+    // ================================================================ mass rows
+    Slot* slots = a.slots + (size_t)row * a.G;
+    // the chunk is kept as the keys of q = z / T (q = f_of_key(key) up to the
+    // sign of zero); its tokens within 40 octaves of its own maximum go to its
+    // region
+    float z[kEPT];
+    load_chunk_pen<DT>(a, p, row, start, end, z, lds, sc);
+    QS_TR(1);
+    u32 kz[kEPT];
+    u32 kmx = 0u, nkmn = 0u, dummy = 0u;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      const u32 k = ((i % VW) < lim[i / VW]) ? skey(z[i] / p.T) : 0u;
+      kz[i] = k;
+      kmx = k > kmx ? k : kmx;
+      nkmn = (k && ~k > nkmn) ? ~k : nkmn;
     }
-    QS_TR(4);
-    // ---- the last workgroup merges and resolves the row
-    u64* s = (u64*)lds;                    // merged candidates [kMergeCap]
-    u32* offs = (u32*)(s + kMergeCap);     // per-workgroup candidate offsets [G]
-    SelLds& SL = *(SelLds*)(offs + kMaxChunks);
-    const Slot* slr = a.slots + (size_t)row * a.G;
-    // per-workgroup counts, thresholds and maxima below them (one load each)
-    const int gper = (a.G + kThreads - 1) / kThreads;
-    u32 cnt_loc = 0, tstar_loc = 0, nout_loc = 0, ovf = 0;
-    for (int q = 0; q < gper; ++q) {
-      const int g = tid * gper + q;
-      if (g < a.G) {
-        const u32 cg = ldc(&slr[g].nb);
-        const u32 tg = ldc(&slr[g].pad[0]);
-        const u32 bg = ldc(&slr[g].pad[1]);
-        if (cg == 0xffffffffu) ovf = 1u;
-        offs[g] = (cg == 0xffffffffu) ? 0u : cg;
-        tstar_loc = tg > tstar_loc ? tg : tstar_loc;
-        nout_loc = bg > nout_loc ? bg : nout_loc;
-      }
-    }
-    __syncthreads();
-    QS_TR(11);
-    for (int q = 0; q < gper; ++q) {
-      const int g = tid * gper + q;
-      if (g < a.G) cnt_loc += offs[g];
-    }
-    const u32 tstar = block_max_u32(tstar_loc, sc);
-    const u32 nout = block_max_u32(nout_loc, sc);
-    const bool overflow = block_max_u32(ovf, sc) != 0u;
-    u32 M;
-    {
-      u32 run = block_scan_u32(cnt_loc, sc, &M);
-      for (int q = 0; q < gper; ++q) {
-        const int g = tid * gper + q;
-        if (g < a.G) {
-          const u32 cg = offs[g];
-          offs[g] = run;
-          run += cg;
-        }
-      }
-    }
+    block_max3(kmx, nkmn, dummy, sc);
+    const u32 kthr_l = window_key(octave_of(f_of_key(kmx)) - kWindow);
+    u32 below;
+    const u32 total = emit_region<DT>(a, row, blk, start, end, kz, kthr_l, sc, &below);
+    QS_TR(2);
     if (tid == 0) {
-      sc.r[3] = 0u;    // merged count
-      sc.r[2] = nout;  // max key outside the merged set
+      const bool fits = total <= (u32)a.R;
+      stc(&slots[blk].nb, fits ? total : 0xffffffffu);
+      maxc(&c->kmax, kmx);
+      maxc(&c->nkmin, nkmn);
+      if (fits) addc(&c->cand_n, total);
+      else orc(&c->status, kStOverflow);
+    }
+    QS_TR(3);
+    row_barrier(c, (u32)a.G, 1u);
+    QS_TR(4);
+    const u32 rkmax = ldc(&c->kmax);
+    const u32 rnkmin = ldc(&c->nkmin);
+    const u32 candn = ldc(&c->cand_n);
+    const u32 st = ldc(&c->status);
+    const int N = octave_of(f_of_key(rkmax));
+    // a timed-out barrier, or a peaked row: k_finish resolves it
+    if ((st & kStTimeout) || (!(st & kStOverflow) && candn <= (u32)kFinCap)) return;
+    // ---- flat row: exact weights, per-bin masses of this chunk
+    const double yhi = y_of(f_of_key(rkmax));
+    double ylo = rnkmin ? y_of(f_of_key(~rnkmin)) : yhi;
+    if (ylo < (double)(N - kWindow)) ylo = (double)(N - kWindow);
+    const double bscale = (yhi > ylo) ? (double)kBins / (yhi - ylo) : 0.0;
+    u64* blo_m = (u64*)lds;          // [kBins] low 32-bit parts of the bin masses
+    u64* bhi_m = blo_m + kBins;      // [kBins] high parts
+    u64* gmh = bhi_m + kBins;        // [kBins] the row's histogram, read back
+    blo_m[tid] = 0ull;
+    bhi_m[tid] = 0ull;
+    __syncthreads();
+    u128 acc = 0;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      u32 ki = kz[i];
+      asm volatile("" : "+v"(ki));
+      const double y = y_of(f_of_key(ki));
+      const u64 w = ki ? weight_y(y, N) : 0ull;
+      if (w) {
+        acc += (u128)w;
+        if (p.topp_on) {
+          const int b = mass_bin(y, ylo, bscale);
+          atomicAdd(&blo_m[b], w & 0xffffffffull);
+          atomicAdd(&bhi_m[b], w >> 32);
+        }
+      }
+    }
+    acc = block_sum128(acc, sc);  // its barriers also order the LDS atomics
+    if (tid == 0) {
+      stc(&slots[blk].s_lo, (u64)acc);
+      stc(&slots[blk].s_hi, (u64)(acc >> 64));
+    }
+    QS_TR(5);
+    if (!p.topp_on) return;  // plain draw: k_finish finds the chunk and the token
+    u64* gh = a.mhist + (size_t)row * kBins;
+    if (bhi_m[tid]) addc(&gh[tid], bhi_m[tid]);
+    row_barrier(c, (u32)a.G, 2u);
+    QS_TR(6);
+    // every workgroup: the total mass, the target and the bracket of bins
+    u128 sv = 0;
+    if (tid < a.G) sv = mk128(ldc(&slots[tid].s_lo), ldc(&slots[tid].s_hi));
+    gmh[tid] = ldc(&gh[tid]);
+    const u128 S = block_sum128(sv, sc);  // its barriers also publish gmh
+    const u128 Tp = mul_frac(S, p.tp);
+    int blo, bhi;
+    bracket_bins(gmh, (u64)a.V, Tp, 32, sc, &blo, &bhi);
+    if (blk == 0 && tid == 0) {
+      stc(&c->tp_lo, (u64)Tp);
+      stc(&c->tp_hi, (u64)(Tp >> 64));
+      stc(&c->flat_blo, (u32)blo);
+    }
+    // this chunk: exact mass above the bracket; its bracketed tokens,
+    // aggregated by key, appended to the row's list as (key, chunk, count)
+    const u128 av = (tid > bhi) ? mk128(blo_m[tid], 0) + ((u128)bhi_m[tid] << 32) : (u128)0;
+    const u128 above = block_sum128(av, sc);
+    u32* stg = (u32*)(gmh + kBins);  // [kHash] keys of the bracketed tokens
+    u32* hk = stg + kHash;           // [kHash] hash table: key
+    u32* hc = hk + kHash;            //                     count
+    for (int i = tid; i < kHash; i += kThreads) {
+      hk[i] = 0u;
+      hc[i] = 0u;
+    }
+    if (tid == 0) sc.r[13] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      u32 ki = kz[i];
+      asm volatile("" : "+v"(ki));  // recomputed here: keeping 32 doubles from the last pass costs registers
+      const double y = y_of(f_of_key(ki));
+      bool in = false;
+      if (ki && floor(y) >= (double)(N - kWindow)) {
+        const int b = mass_bin(y, ylo, bscale);
+        in = b >= blo && b <= bhi;
+      }
+      const u32 slot = wave_append(in, &sc.r[13]);
+      if (in && slot < (u32)kHash) stg[slot] = ki;
     }
     __syncthreads();
-    QS_TR(12);
-    bool ok = !overflow;
-    if (ok) {
-      // each thread takes a contiguous run of the M emitted candidates (in
-      // workgroup order); all its loads are issued before any is used
-      const u64* cd = a.cand + (size_t)row * a.G * kBlockCand;
-      const u32 per = (M + kThreads - 1) / kThreads;
-      for (u32 base = 0; base < per; base += 16) {
-        const u32 f0 = (u32)tid * per + base;
-        u64 vals[16];
-        int g = 0;
-        if (f0 < M) {
-          int lo = 0, hi = a.G - 1;  // last g with offs[g] <= f0
-          while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (offs[mid] <= f0) lo = mid; else hi = mid - 1;
-          }
-          g = lo;
+    const u32 nbt = sc.r[13];
+    const u32 nst = nbt < (u32)kHash ? nbt : (u32)kHash;
+    for (u32 s = tid; s < nst; s += kThreads) {
+      const u32 key = stg[s];
+      u32 h = (key * 0x9E3779B1u) >> 22;  // kHash = 1024 slots
+      for (int probe = 0; probe < kHash; ++probe) {
+        const u32 prev = atomicCAS(&hk[h], 0u, key);
+        if (prev == 0u || prev == key) {
+          atomicAdd(&hc[h], 1u);
+          break;
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const u32 f = f0 + (u32)r;
-          const bool valid = (base + (u32)r < per) && f < M;
-          if (valid)
-            while (g + 1 < a.G && offs[g + 1] <= f) ++g;
-          vals[r] = valid ? ldc(&cd[(size_t)g * kBlockCand + (f - offs[g])]) : 0ull;
-        }
-        u32 outmax = 0u;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const u32 f = f0 + (u32)r;
-          const bool valid = (base + (u32)r < per) && f < M;
-          const u32 k = (u32)(vals[r] >> 32);
-          const bool take = valid && k >= tstar;
-          const u32 slot = wave_append(take, &sc.r[3]);
-          if (take && slot < (u32)kMergeCap) s[slot] = vals[r];
-          if (valid && !take) outmax = k > outmax ? k : outmax;
-        }
-        outmax = wave_max(outmax);
-        if ((tid & 63) == 0 && outmax) atomicMax(&sc.r[2], outmax);
+        h = (h + 1u) & (u32)(kHash - 1);
       }
-      __syncthreads();
-      const u32 m = sc.r[3];
-      const u32 zout = sc.r[2];
-      __syncthreads();
-      QS_TR(5);
-      ok = m <= (u32)kMergeCap && finish_topk(a, p, row, s, (int)m, zout, SL, sc);
     }
-    if (!ok) {
-      if (DT == QS_DTYPE_F32) resolve_single<QS_DTYPE_F32>(a, p, row, lds, sc);
-      else resolve_single<QS_DTYPE_BF16>(a, p, row, lds, sc);
+    __syncthreads();
+    u32 ne = 0u;
+#pragma unroll
+    for (int q = 0; q < kHash / kThreads; ++q) ne += hc[tid * (kHash / kThreads) + q] ? 1u : 0u;
+    u32 net;
+    const u32 neoff = block_scan_u32(ne, sc, &net);
+    if (tid == 0) {
+      stc(&slots[blk].a_lo, (u64)above);
+      stc(&slots[blk].a_hi, (u64)(above >> 64));
+      stc(&slots[blk].nbr, nbt);
+      if (nbt > (u32)kHash) orc(&c->status, kStList);
+      sc.r[12] = net ? addc(&c->list_n, net) : 0u;
+    }
+    __syncthreads();
+    const u32 base = sc.r[12];
+    if (net && nbt <= (u32)kHash && (u64)base + net <= (u64)kListCap) {
+      u64* lst = a.list + (size_t)row * kListCap + base + neoff;
+      u32 pos = 0u;
+#pragma unroll
+      for (int q = 0; q < kHash / kThreads; ++q) {
+        const int h = tid * (kHash / kThreads) + q;
+        const u32 n = hc[h];
+        if (n) {
+          u32* ent = (u32*)&lst[pos];
+          stc(&ent[0], ((u32)blk << 16) | n);
+          stc(&ent[1], hk[h]);
+          ++pos;
+        }
+      }
     }
     QS_TR(7);
+  }
+}
+
+// ---------------------------------------------------------------- finishing kernel
+
+// One workgroup per row, after k_sample of the same ROLE: resolves the rows
+// k_sample left open and returns their counters to zero.
+//   ROLE 0: top-k rows from the regions; rows with large k, and mass rows when
+//           no mass launch runs, by resolve_single.
+//   ROLE 1: mass rows: peaked rows from the regions, flat rows from the
+//           bracketed tokens and the chunk holding the draw.
+template <int DT, int ROLE>
+__global__ __launch_bounds__(kThreads) void k_finish(Args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  __shared__ Scratch sc;
+  const int row = blockIdx.x;
+  const RowParams p = row_params(a, row);
+  RowCtl* c = a.ctl + row;
+#ifdef QS_TRACE
+  if (threadIdx.x == 0) sc.tslot = (u32)(a.B * a.G + row);
+#endif
+  if (ROLE == 0) {
+    if (p.kind == kGreedy || (p.kind == kMass && !(a.flags & QS_FLAG_NO_MASS_ROWS))) return;
+    QS_TR(0);
+    if (p.kind == kTopK) {
+      if (!finish_row<true>(a, p, row, 0u, lds, sc)) resolve_single<DT>(a, p, row, lds, sc);
+    } else {
+      give_up(a, row, kWhyLargeK);
+      resolve_single<DT>(a, p, row, lds, sc);
+    }
     reset_row(a, row);
     QS_TR(15);
     return;
   }
+  if (p.kind != kMass) return;
+  QS_TR(0);
+  const u32 st = ldc(&c->status);
+  const u32 candn = ldc(&c->cand_n);
+  const int N = octave_of(f_of_key(ldc(&c->kmax)));
+  bool hist = false;
+  if (st & kStTimeout) {
+    give_up(a, row, kWhyTimeout);
+    resolve_single<DT>(a, p, row, lds, sc);
+  } else if (!(st & kStOverflow) && candn <= (u32)kFinCap) {
+    if (!finish_row<false>(a, p, row, window_key(N - kWindow), lds, sc)) resolve_single<DT>(a, p, row, lds, sc);
   } else {
-  // ================================================================ mass rows
-  MassLds& M = *(MassLds*)lds;
-  Slot* slots = a.slots + (size_t)row * a.G;
-  // q = z / T; key range of the row
-  u32 kmx = 0u, kmn = 0xffffffffu;
-  QS_FOR_ELEMS({
-    zz = zz / p.T;
-    const u32 k = skey(zz);
-    kmx = k > kmx ? k : kmx;
-    kmn = k < kmn ? k : kmn;
-  })
-  kmx = block_max_u32(kmx, sc);
-  kmn = ~block_max_u32(~kmn, sc);
-  QS_TR(2);
-  if (tid == 0) {
-    maxc(&c->kmax, kmx);
-    maxc(&c->nkmin, ~kmn);
+    hist = p.topp_on;
+    const u128 Tp = p.topp_on ? mk128(ldc(&c->tp_lo), ldc(&c->tp_hi)) : (u128)0;
+    const bool bottom = !p.topp_on || ldc(&c->flat_blo) == 0u;
+    if (!resolve_flat<DT>(a, p, row, N, p.topp_on, Tp, bottom, lds, sc)) resolve_single<DT>(a, p, row, lds, sc);
   }
-  QS_TR(3);
-  row_barrier(c, (u32)a.G, 1u);
-  QS_TR(4);
-  const u32 rkmax = ldc(&c->kmax);
-  const u32 rkmin = ~ldc(&c->nkmin);
-  const float qmax = f_of_key(rkmax);
-  const int N = octave_of(qmax);
-  u128 W = 0;
-  u32 kappa_p = 0u, id_p = 0xffffffffu;  // kept: key > kappa_p || (key == kappa_p && id <= id_p)
-  bool failed = false;
-  bool single_key = false;
-  u32 bkey = 0u;
-  u64 bw = 0ull;     // weight of the single bracket key
-  u64 jkeep = 0ull;  // single key: bracketed tokens kept, in id order
-
-  if (!p.topp_on) {
-    // ---- plain draw: chunk masses
-    u128 acc = 0;
-    QS_FOR_ELEMS({ acc += (u128)weight_of(zz, N); })
-    acc = block_sum128(acc, sc);
-    if (tid == 0) {
-      stc(&slots[blk].s_lo, (u64)acc);
-      stc(&slots[blk].s_hi, (u64)(acc >> 64));
-    }
-    row_barrier(c, (u32)a.G, 2u);
-    QS_TR(5);
-    load_slots(M, slots, a.G);
-    u128 v = 0;
-    for (int g = tid; g < a.G; g += kThreads) v += mk128(M.a_lo[g], M.a_hi[g]);
-    W = block_sum128(v, sc);
-  } else {
-    // ---- level 1: histogram over y in [ylo, yhi]
-    const double yhi = y_of(qmax);
-    double ylo = y_of(f_of_key(rkmin));
-    if (ylo < (double)(N - kWindow)) ylo = (double)(N - kWindow);
-    const double sc1 = (yhi > ylo) ? (double)kBins / (yhi - ylo) : 0.0;
-    for (int i = tid; i < kBins; i += kThreads) M.h[i] = 0ull;
-    __syncthreads();
-    u128 acc = 0;
-    QS_FOR_ELEMS({
-      const double y = y_of(zz);
-      const u64 w = weight_y(y, N);
-      if (w) {
-        acc += (u128)w;
-        const int b = min(kBins - 1, (int)((y - ylo) * sc1));
-        atomicAdd(&M.h[b], w >> 24);
-      }
-    })
-    acc = block_sum128(acc, sc);  // its __syncthreads also orders the LDS atomics
-    if (tid == 0) {
-      stc(&slots[blk].s_lo, (u64)acc);
-      stc(&slots[blk].s_hi, (u64)(acc >> 64));
-    }
-    u64* gh1 = a.mhist + (size_t)row * 2 * kBins;
-    for (int i = tid; i < kBins; i += kThreads)
-      if (M.h[i]) addc(&gh1[i], M.h[i]);
-    row_barrier(c, (u32)a.G, 2u);
-    QS_TR(5);
-    // total mass S, the target, and the level-1 bracket
-    load_slots(M, slots, a.G);
-    u128 sv = 0;
-    for (int g = tid; g < a.G; g += kThreads) sv += mk128(M.a_lo[g], M.a_hi[g]);
-    const u128 S = block_sum128(sv, sc);
-    const u128 Tp = mul_frac(S, p.tp);
-    for (int i = tid; i < kBins; i += kThreads) M.g[i] = ldc(&gh1[i]);
-    __syncthreads();
-    const u64 err = (u64)a.V;  // each token truncates less than one unit
-    int blo1, bhi1, blo2, bhi2;
-    bracket_bins(M.g, 0ull, err, Tp, sc, &blo1, &bhi1);
-    u64 above1;
-    {
-      const int b = kBins - 1 - tid;
-      const u64 v = b > bhi1 ? M.g[b] : 0ull;
-      above1 = (u64)acc_mass(block_sum_acc(acc_of((u128)v, 0u), sc));
-    }
-    // ---- level 2: histogram inside the level-1 bracket
-    const double w1 = (sc1 > 0.0) ? 1.0 / sc1 : 0.0;
-    const double ylo2 = ylo + (double)blo1 * w1;
-    const double yhi2 = ylo + (double)(bhi1 + 1) * w1;
-    const double sc2 = (sc1 > 0.0 && yhi2 > ylo2) ? (double)kBins / (yhi2 - ylo2) : 0.0;
-    __syncthreads();
-    for (int i = tid; i < kBins; i += kThreads) M.h[i] = 0ull;
-    __syncthreads();
-    QS_FOR_ELEMS({
-      const double y = y_of(zz);
-      const u64 w = weight_y(y, N);
-      if (w) {
-        const int b1 = min(kBins - 1, (int)((y - ylo) * sc1));
-        if (b1 >= blo1 && b1 <= bhi1) {
-          int b2 = (int)((y - ylo2) * sc2);
-          b2 = b2 < 0 ? 0 : (b2 > kBins - 1 ? kBins - 1 : b2);
-          atomicAdd(&M.h[b2], w >> 24);
-        }
-      }
-    })
-    __syncthreads();
-    u64* gh2 = gh1 + kBins;
-    for (int i = tid; i < kBins; i += kThreads)
-      if (M.h[i]) addc(&gh2[i], M.h[i]);
-    row_barrier(c, (u32)a.G, 3u);
-    QS_TR(6);
-    for (int i = tid; i < kBins; i += kThreads) M.g[i] = ldc(&gh2[i]);
-    __syncthreads();
-    bracket_bins(M.g, above1, err, Tp, sc, &blo2, &bhi2);
-    __syncthreads();
-    // ---- exact: mass above the bracket; bracketed tokens listed
-    u128 accA = 0;
-    u32 nb = 0, bkmx = 0u, bkmn = 0xffffffffu;
-    QS_FOR_ELEMS({
-      const double y = y_of(zz);
-      const u64 w = weight_y(y, N);
-      if (w) {
-        const int b1 = min(kBins - 1, (int)((y - ylo) * sc1));
-        bool above = b1 > bhi1, inside = false;
-        if (b1 >= blo1 && b1 <= bhi1) {
-          int b2 = (int)((y - ylo2) * sc2);
-          b2 = b2 < 0 ? 0 : (b2 > kBins - 1 ? kBins - 1 : b2);
-          above = b2 > bhi2;
-          inside = b2 >= blo2 && b2 <= bhi2;
-        }
-        if (above) accA += (u128)w;
-        if (inside) {
-          const u32 k = skey(zz);
-          ++nb;
-          bkmx = k > bkmx ? k : bkmx;
-          bkmn = k < bkmn ? k : bkmn;
-        }
-      }
-    })
-    accA = block_sum128(accA, sc);
-    bkmx = block_max_u32(bkmx, sc);
-    bkmn = ~block_max_u32(~bkmn, sc);
-    u32 nbt;
-    const u32 nboff = block_scan_u32(nb, sc, &nbt);
-    if (tid == 0) {
-      stc(&slots[blk].s_lo, (u64)accA);
-      stc(&slots[blk].s_hi, (u64)(accA >> 64));
-      stc(&slots[blk].nb, nbt);
-      if (nbt) {
-        maxc(&c->brk_kmax, bkmx);
-        maxc(&c->brk_nkmin, ~bkmn);
-        sc.r[4] = addc(&c->brk_n, nbt);
-      }
-    }
-    __syncthreads();
-    const u32 bbase = sc.r[4];
-    if (nbt && (u64)bbase + nbt <= (u64)kBracketCap) {
-      u64* bl = a.brk + (size_t)row * kBracketCap + bbase + nboff;
-      u32 pos = 0;
-      QS_FOR_ELEMS({
-        const double y = y_of(zz);
-        if (weight_y(y, N)) {
-          const int b1 = min(kBins - 1, (int)((y - ylo) * sc1));
-          if (b1 >= blo1 && b1 <= bhi1) {
-            int b2 = (int)((y - ylo2) * sc2);
-            b2 = b2 < 0 ? 0 : (b2 > kBins - 1 ? kBins - 1 : b2);
-            if (b2 >= blo2 && b2 <= bhi2) {
-              stc(&bl[pos], ((u64)skey(zz) << 32) | (0xffffffffu - (u32)e));
-              ++pos;
-            }
-          }
-        }
-      })
-    }
-    row_barrier(c, (u32)a.G, 4u);
-    QS_TR(7);
-    // ---- every workgroup resolves the boundary from the published data
-    load_slots(M, slots, a.G);
-    u128 av = 0;
-    for (int g = tid; g < a.G; g += kThreads) av += mk128(M.a_lo[g], M.a_hi[g]);
-    const u128 A = block_sum128(av, sc);
-    const u32 nbr = ldc(&c->brk_n);
-    const u32 gkmx = ldc(&c->brk_kmax), gkmn = ~ldc(&c->brk_nkmin);
-    const bool bottom = (blo1 == 0 && blo2 == 0);
-    if (A > Tp || nbr == 0u) {
-      failed = true;
-    } else if (gkmx == gkmn) {
-      // one key in the bracket: all bracketed tokens weigh the same
-      single_key = true;
-      bkey = gkmx;
-      bw = weight_of(f_of_key(bkey), N);
-      // bracketed tokens with exclusive mass <= Tp: floor((Tp - A) / bw) + 1, at most nbr
-      u64 j = nbr;
-      if (Tp - A < (u128)bw * nbr) j = div_small(Tp - A, bw) + 1ull;
-      if (j >= nbr) {
-        j = nbr;
-        if (A + (u128)bw * nbr <= Tp && !bottom) failed = true;
-      }
-      jkeep = j;
-      W = A + (u128)bw * j;
-      kappa_p = bkey;
-    } else if (nbr > (u32)kBracketCap) {
-      failed = true;
-    } else {
-      // the bracketed tokens in LDS (loads issued before use), then radix
-      // selects: the boundary by mass, the boundary member among ties by id
-      const u64* bl = a.brk + (size_t)row * kBracketCap;
-      const int nn = (int)nbr;
-      {
-        constexpr int kPerT = kBracketCap / kThreads;
-        u64 tmp[kPerT];
-#pragma unroll
-        for (int q = 0; q < kPerT; ++q) {
-          const int i = q * kThreads + tid;
-          tmp[q] = i < nn ? ldc(&bl[i]) : 0ull;
-        }
-#pragma unroll
-        for (int q = 0; q < kPerT; ++q) {
-          const int i = q * kThreads + tid;
-          if (i < nn) M.list[i] = tmp[q];
-        }
-      }
-      __syncthreads();
-      auto key = [&](int i) { return (u32)(M.list[i] >> 32); };
-      auto idof = [&](int i) { return 0xffffffffu - (u32)M.list[i]; };
-      auto all = [&](int) { return true; };
-      auto nowt = [&](int) { return 0ull; };
-      auto wt = [&](int i) { return weight_of(f_of_key(key(i)), N); };
-      const SelOut sp = lds_select<true, true>(nn, key, all, wt, Tp - A, M.sel, sc);
-      if (!sp.ok) {
-        // every bracketed token is kept: only right if nothing with weight lies below
-        if (!bottom) failed = true;
-        kappa_p = 0u;
-        id_p = 0xffffffffu;
-      } else {
-        kappa_p = sp.val;
-        const u128 A2 = A + acc_mass(sp.before);
-        const u64 wk = weight_of(f_of_key(kappa_p), N);
-        const u64 j = div_small(Tp - A2, wk);  // 0-based boundary member among the ties
-        if (j + 1 < sp.at.c) {
-          auto intie = [&](int i) { return key(i) == kappa_p; };
-          const SelOut si = lds_select<false, false>(nn, idof, intie, nowt, (u128)j, M.sel, sc);
-          if (!si.ok) failed = true;
-          id_p = si.val;
-        }
-      }
-      if (!failed) {
-        // per-chunk mass of the kept bracketed tokens
-        for (int g = tid; g < a.G; g += kThreads) {
-          M.c_lo[g] = 0ull;
-          M.c_hi[g] = 0ull;
-        }
-        __syncthreads();
-        for (int i = tid; i < nn; i += kThreads) {
-          const u32 k = key(i), id = idof(i);
-          if (k > kappa_p || (k == kappa_p && id <= id_p)) {
-            const u64 w = wt(i);
-            const int ch = (int)(id / (u32)a.CH);
-            atomicAdd(&M.c_lo[ch], w & 0xffffffffull);
-            atomicAdd(&M.c_hi[ch], w >> 32);
-          }
-        }
-        __syncthreads();
-        u128 wv = 0;
-        for (int g = tid; g < a.G; g += kThreads) wv += mk128(M.c_lo[g], 0) + ((u128)M.c_hi[g] << 32);
-        W = A + block_sum128(wv, sc);
-      }
-    }
-  }
-
-  if (failed) {
-    QS_TR(9);
-    if (blk == 0) {
-      if (DT == QS_DTYPE_F32) resolve_single<QS_DTYPE_F32>(a, p, row, lds, sc);
-      else resolve_single<QS_DTYPE_BF16>(a, p, row, lds, sc);
-    }
-    if (arrive_last(c, (u32)a.G, sc)) reset_row(a, row);
-    return;
-  }
-
-  // ---- the draw: kept mass per chunk, the chunk holding the target, then
-  // that workgroup locates the token in id order
-  const u128 t = mul_frac(W, p.u);
-  const bool need_rank = p.topp_on && single_key;
-  {
-    // one chunk per thread (G <= kMaxChunks <= kThreads)
-    const int g = tid;
-    u32 nbg = 0;
-    u128 wg = 0;
-    if (g < a.G) {
-      wg = mk128(M.a_lo[g], M.a_hi[g]);
-      nbg = need_rank ? M.nbv[g] : 0u;
-    }
-    u32 nbtot;
-    const u32 before = block_scan_u32(nbg, sc, &nbtot);
-    if (g < a.G) {
-      M.pref[g] = before;
-      if (p.topp_on) {
-        if (single_key) {
-          const u64 keep = jkeep > before ? min((u64)nbg, jkeep - before) : 0ull;
-          wg += (u128)bw * keep;
-        } else {
-          wg += mk128(M.c_lo[g], 0) + ((u128)M.c_hi[g] << 32);
-        }
-      }
-    }
-    Acc tot;
-    const Acc ex = block_scan_acc(acc_of(wg, 0u), sc, &tot);
-    if (tid == 0) sc.r[5] = (u32)(a.G - 1);  // unreachable fallback: t < W
-    __syncthreads();
-    if (g < a.G && t >= acc_mass(ex) && t < acc_mass(ex) + wg) {
-      sc.r[5] = (u32)g;
-      const u128 tl = t - acc_mass(ex);
-      sc.w[3 * kWaves] = (u64)tl;
-      sc.w[3 * kWaves + 1] = (u64)(tl >> 64);
-    }
-    __syncthreads();
-  }
-  const int owner = (int)sc.r[5];
-  const u128 tloc = (owner == (int)sc.r[5]) ? mk128(sc.w[3 * kWaves], sc.w[3 * kWaves + 1]) : 0;
-  __syncthreads();
-  // single key: this chunk's kept bracketed tokens are its first `kmine` members in id order
-  u64 kmine = 0ull;
-  bool idp_me = false;
-  if (need_rank) {
-    const u64 before = M.pref[blk];
-    const u64 nbme = M.nbv[blk];
-    kmine = jkeep > before ? min(nbme, jkeep - before) : 0ull;
-    // the workgroup holding the last kept member records its id (for k_probs)
-    idp_me = jkeep > before && jkeep <= before + nbme;
-  }
-  const bool owner_me = (owner == blk);
-  QS_TR(8);
-  if (owner_me || idp_me) {
-    // One pass over the chunk in id order, which is (v, thread, j).  Per v:
-    // ranks of the single bracket key's members (id order), the kept mass,
-    // and, in the vector that holds the draw target, the drawn token.
-    u128 rem = tloc;
-    u32 members = 0;  // members of the bracket key in earlier vectors
-    bool found = false;
-    if (tid == 0) {
-      sc.r[1] = 0xffffffffu;
-      sc.r[2] = 0xffffffffu;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      u32 rank = 0;
-      if (need_rank) {
-        u32 mc = 0;
-#pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          const int e = start + (v * kThreads + tid) * VW + j;
-          if (e < end && skey(z[v * VW + j]) == bkey && weight_of(z[v * VW + j], N)) ++mc;
-        }
-        u32 mtot;
-        rank = members + block_scan_u32(mc, sc, &mtot);
-        members += mtot;
-      }
-      // kept mass of this thread's tokens in vector v (and the boundary member for k_probs)
-      u128 part = 0;
-      {
-        u32 r = rank;
-#pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          const int e = start + (v * kThreads + tid) * VW + j;
-          if (e < end) {
-            const float q = z[v * VW + j];
-            const u32 k = skey(q);
-            const u64 w = weight_of(q, N);
-            bool kept;
-            if (!p.topp_on) {
-              kept = true;
-            } else if (single_key) {
-              if (k == bkey && w) {
-                kept = (u64)r < kmine;
-                if (idp_me && (u64)r + 1 == kmine) sc.r[2] = (u32)e;
-                ++r;
-              } else {
-                kept = k > bkey;
-              }
-            } else {
-              kept = k > kappa_p || (k == kappa_p && (u32)e <= id_p);
-            }
-            if (kept) part += (u128)w;
-          }
-        }
-      }
-      if (owner_me && !found) {
-        Acc tot;
-        const Acc ex = block_scan_acc(acc_of(part, 0u), sc, &tot);
-        const u128 tv = acc_mass(tot);
-        if (rem < tv) {
-          found = true;
-          const u128 lo = acc_mass(ex);
-          if (rem >= lo && rem < lo + part) {
-            u128 runm = lo;
-            u32 r = rank;
-#pragma unroll
-            for (int j = 0; j < VW; ++j) {
-              const int e = start + (v * kThreads + tid) * VW + j;
-              if (e < end) {
-                const float q = z[v * VW + j];
-                const u32 k = skey(q);
-                const u64 w = weight_of(q, N);
-                bool kept;
-                if (!p.topp_on) {
-                  kept = true;
-                } else if (single_key) {
-                  if (k == bkey && w) {
-                    kept = (u64)r < kmine;
-                    ++r;
-                  } else {
-                    kept = k > bkey;
-                  }
-                } else {
-                  kept = k > kappa_p || (k == kappa_p && (u32)e <= id_p);
-                }
-                if (kept) {
-                  runm += (u128)w;
-                  if (runm > rem && sc.r[1] == 0xffffffffu) sc.r[1] = (u32)e;
-                }
-              }
-            }
-          }
-        } else {
-          rem -= tv;
-        }
-      }
-    }
-    __syncthreads();
-    if (tid == 0) {
-      RowCtl* cc = a.ctl + row;
-      if (idp_me) cc->id_p = sc.r[2];
-      if (owner_me) {
-        // a timed-out row barrier leaves the row unresolved: report an invalid id
-        if (ldc(&c->status) & kStTimeout) sc.r[1] = 0xffffffffu;
-        a.out_ids[row] = (sc.r[1] == 0xffffffffu) ? -1ll : (long long)sc.r[1];
-        cc->chosen = (long long)sc.r[1];
-        cc->n_max = N;
-        cc->w_lo = (u64)W;
-        cc->w_hi = (u64)(W >> 64);
-        cc->greedy = 0u;
-        cc->path = 2u;
-        cc->kappa_p = single_key ? bkey : kappa_p;
-        if (!single_key) cc->id_p = id_p;
-      }
-    }
-    __syncthreads();
-  }
-  QS_TR(10);
-  if (arrive_last(c, (u32)a.G, sc)) reset_row(a, row);
+  reset_row(a, row, hist);
   QS_TR(15);
-  }
-#undef QS_FOR_ELEMS
 }
 
 // ---------------------------------------------------------------- probabilities
@@ -1856,13 +2154,13 @@ __global__ __launch_bounds__(kThreads) void k_probs(Args a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   __shared__ Scratch sc;
   const int row = blockIdx.y, blk = blockIdx.x;
-  const int start = blk * a.CH, end = min(a.V, start + a.CH);
+  const int start = blk * kCH, end = min(a.V, start + kCH);
   RowCtl* c = a.ctl + row;
   const RowParams p = row_params(a, row);
   PenTable pt;
   pt.bits = (u32*)lds;
-  pt.wpre = pt.bits + (a.CH >> 5);
-  pt.cnts = pt.wpre + (a.CH >> 5);
+  pt.wpre = pt.bits + (kCH >> 5);
+  pt.cnts = pt.wpre + (kCH >> 5);
   if (p.pen_on && !p.greedy) pen_build(a, row, start, end, pt, sc);
   const long long chosen = c->chosen;
   u32 kept = 0;
@@ -1922,62 +2220,60 @@ int fail(const char* fmt, const char* detail = "") {
 }
 
 struct Layout {
-  int EPT, CH, G, seg_cap, Hpad;
-  size_t off_ctl, off_cand, off_hist, off_brk, off_slots, total;
-  size_t lds;
+  int G, R, logR, seg_cap, Hpad;
+  size_t off_ctl, off_cand, off_hist, off_list, off_slots, total;
+  size_t lds_sample, lds_finish;
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Elements per thread: 32 once the batch has enough chunks to fill the chip,
-// else 16 (shorter chunks, more workgroups per row).
-int pick_ept(int B, int V) {
-  const int g32 = (V + kThreads * 32 - 1) / (kThreads * 32);
-  if ((long long)B * g32 >= 512) return 32;
-  return 16;
-}
-
 Layout layout_for(int B, int V, int H) {
   Layout L;
-  L.EPT = pick_ept(B, V);
-  L.CH = kThreads * L.EPT;
-  L.G = (V + L.CH - 1) / L.CH;
-  L.seg_cap = H > 0 ? (H < L.CH ? H : L.CH) : 0;
+  L.G = (V + kCH - 1) / kCH;
+  // region capacity: the largest power of two with G * R <= kRegionTotal
+  L.R = 1;
+  L.logR = 0;
+  while (L.G * (L.R * 2) <= kRegionTotal) {
+    L.R *= 2;
+    ++L.logR;
+  }
+  L.seg_cap = H > 0 ? (H < kCH ? H : kCH) : 0;
   L.Hpad = 1;
   while (L.Hpad < H) L.Hpad <<= 1;
   size_t o = 0;
   L.off_ctl = o;
   o = align_up(o + (size_t)B * sizeof(RowCtl), 256);
   L.off_cand = o;
-  o = align_up(o + (size_t)B * L.G * kBlockCand * 8, 256);
+  o = align_up(o + (size_t)B * L.G * L.R * 8, 256);
   L.off_hist = o;
-  o = align_up(o + (size_t)B * 2 * kBins * 8, 256);
-  L.off_brk = o;
-  o = align_up(o + (size_t)B * kBracketCap * 8, 256);
+  o = align_up(o + (size_t)B * kBins * 8, 256);
+  L.off_list = o;
+  o = align_up(o + (size_t)B * kListCap * 8, 256);
   L.off_slots = o;
   o = align_up(o + (size_t)B * L.G * sizeof(Slot), 256);
   L.total = o;
-  const size_t pen = H > 0 ? (size_t)(2 * (L.CH / 32) + L.seg_cap) * 4 : 0;
-  const size_t merge = (size_t)kMergeCap * 8 + (size_t)kMaxChunks * 4 + sizeof(SelLds);
+  const size_t pen = H > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 0;
+  const size_t fin = (size_t)kFinCap * 8;  // staging, then 2 * SelLds
+  const size_t flat = sizeof(FlatLds);
   const size_t single = sizeof(SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
-  const size_t mass = sizeof(MassLds);
-  L.lds = pen;
-  if (merge > L.lds) L.lds = merge;
-  if (single > L.lds) L.lds = single;
-  if (mass > L.lds) L.lds = mass;
+  const size_t bins = (size_t)3 * kBins * 8 + (size_t)3 * kHash * 4;  // flat mass rows in k_sample
+  L.lds_sample = pen > bins ? pen : bins;
+  L.lds_finish = pen;
+  if (fin > L.lds_finish) L.lds_finish = fin;
+  if (flat > L.lds_finish) L.lds_finish = flat;
+  if (single > L.lds_finish) L.lds_finish = single;
   return L;
 }
+static_assert(2 * sizeof(SelLds) <= (size_t)kFinCap * 8, "select buffers fit the staging area");
 
-template <int DT, int EPT, int ROLE>
-hipError_t launch_sample(const Args& a, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((k_sample<DT, EPT, ROLE>), dim3(a.G, a.B), dim3(kThreads), lds, st, a);
-  return hipGetLastError();
-}
-
+// k_sample then, unless every row is greedy, k_finish, on one stream.
 template <int DT, int ROLE>
-hipError_t launch_dt(const Args& a, int ept, size_t lds, hipStream_t st) {
-  if (ept == 32) return launch_sample<DT, 32, ROLE>(a, lds, st);
-  return launch_sample<DT, 16, ROLE>(a, lds, st);
+hipError_t launch_role(const Args& a, const Layout& L, bool finish, hipStream_t st) {
+  hipLaunchKernelGGL((k_sample<DT, ROLE>), dim3(a.G, a.B), dim3(kThreads), L.lds_sample, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !finish) return e;
+  hipLaunchKernelGGL((k_finish<DT, ROLE>), dim3(a.B), dim3(kThreads), L.lds_finish, st, a);
+  return hipGetLastError();
 }
 
 #ifdef QS_TRACE
@@ -2028,13 +2324,13 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   if (H > kMaxHistory) return fail("qs_sample: history longer than QS_MAX_HISTORY%s");
   if (out_kept && !out_probs) return fail("qs_sample: out_kept requires out_probs%s");
   const int Heff = hist ? H : 0;
+  if ((V + kCH - 1) / kCH > kMaxChunks) return fail("qs_sample: V too large for the chunking%s");
   const Layout L = layout_for(B, V, Heff);
   if (ws_bytes < L.total) return fail("qs_sample: workspace too small (see qs_workspace_bytes)%s");
   if (((uintptr_t)ws) % 256) return fail("qs_sample: workspace must be 256-byte aligned%s");
   const bool all_greedy = (flags & QS_FLAG_ALL_GREEDY) != 0;
   if (!all_greedy && !uniforms) return fail("qs_sample: uniforms required unless all rows are greedy%s");
-  if (L.G > kMaxChunks) return fail("qs_sample: V too large for the chunking%s");
-  if (L.lds > 64 * 1024) return fail("qs_sample: LDS budget exceeded%s");
+  if (L.lds_sample > 64 * 1024 || L.lds_finish > 64 * 1024) return fail("qs_sample: LDS budget exceeded%s");
 
   Args a;
   memset(&a, 0, sizeof(a));
@@ -2044,7 +2340,8 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   a.V = V;
   a.H = Heff;
   a.G = L.G;
-  a.CH = L.CH;
+  a.R = L.R;
+  a.logR = L.logR;
   a.seg_cap = L.seg_cap;
   a.Hpad = L.Hpad;
   a.flags = flags;
@@ -2063,7 +2360,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   a.ctl = (RowCtl*)(base + L.off_ctl);
   a.cand = (u64*)(base + L.off_cand);
   a.mhist = (u64*)(base + L.off_hist);
-  a.brk = (u64*)(base + L.off_brk);
+  a.list = (u64*)(base + L.off_list);
   a.slots = (Slot*)(base + L.off_slots);
 #ifdef QS_TRACE
   a.trace = g_trace;
@@ -2080,20 +2377,20 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
     e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
     if (e != hipSuccess) return fail("qs_sample: fork failed: %s", hipGetErrorString(e));
+    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, side->stream)
+                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, side->stream);
+    if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
   }
-  e = dtype == QS_DTYPE_F32 ? launch_dt<QS_DTYPE_F32, 0>(a, L.EPT, L.lds, stream)
-                            : launch_dt<QS_DTYPE_BF16, 0>(a, L.EPT, L.lds, stream);
+  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, stream)
+                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, stream);
   if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
   if (mass) {
-    e = dtype == QS_DTYPE_F32 ? launch_dt<QS_DTYPE_F32, 1>(a, L.EPT, L.lds, side->stream)
-                              : launch_dt<QS_DTYPE_BF16, 1>(a, L.EPT, L.lds, side->stream);
-    if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
     e = hipEventRecord(side->join, side->stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
     if (e != hipSuccess) return fail("qs_sample: join failed: %s", hipGetErrorString(e));
   }
   if (out_probs) {
-    const size_t plds = Heff > 0 ? (size_t)(2 * (L.CH / 32) + L.seg_cap) * 4 : 16;
+    const size_t plds = Heff > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 16;
     if (dtype == QS_DTYPE_F32)
       hipLaunchKernelGGL(k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(kThreads), plds, stream, a);
     else
@@ -2108,10 +2405,11 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
 
 extern "C" {
 
-int qs_version(void) { return 200; }
+int qs_version(void) { return 300; }
 
 #ifdef QS_TRACE
-// Trace builds only: device buffer of [B, G, 16] u64 wall-clock stamps.
+// Trace builds only: device buffer of [B * G + B, 16] u64 wall-clock stamps
+// (k_sample workgroups, then k_finish rows).
 void qs_debug_set_trace(void* buf) { g_trace = (u64*)buf; }
 #endif
 
