@@ -58,11 +58,14 @@ constexpr int kWindow = 40;
 constexpr double kYClamp = 1073741824.0;  // 2^30
 constexpr double kLog2e = 1.4426950408889634074;
 constexpr int kTopkFast = QS_TOPK_FAST_MAX;
-constexpr int kGatherPer = 32;                    // region entries one finishing thread loads
-constexpr int kRegionTotal = kThreads * kGatherPer;  // G * R <= this
+constexpr int kGatherPer = 16;                    // region entries one finishing thread loads
+constexpr int kRegionTotal = 8192;                // G * R <= this (the entries written stay <= kThreads * kGatherPer)
 constexpr int kFinPer = 16;                       // merged candidates per thread
 constexpr int kFinCap = kThreads * kFinPer;       // merged candidates per row
 constexpr int kBins = 256;                        // histogram bins
+constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
+constexpr int kWide = 1 << kWideBits;
+constexpr int kWidePer = kWide / kThreads;        // bins per thread
 constexpr int kListCap = kFinCap;                 // bracket entries per row (flat mass rows)
 constexpr int kHash = 1024;                       // bracketed tokens per chunk (flat mass rows)
 constexpr int kMaxChunks = 256;                   // chunks per row (G)
@@ -144,7 +147,7 @@ struct Args {
   float* out_probs;
   int* out_kept;
   RowCtl* ctl;
-  u64* cand;   // [B, G, R] region entries (key << 32 | id)
+  uint4* cand; // [B, G, R] region entries {id, q key, exp2 mantissa M, octave n}
   u64* mhist;  // [B, kBins] global mass histogram (flat mass rows)
   u64* list;   // [B, kListCap] bracket entries (key << 32 | chunk << 16 | count), flat mass rows
   Slot* slots; // [B, G]
@@ -581,6 +584,56 @@ struct SelLds {  // one 8-bit digit level of a radix select
   u64 mlo[256];  // sums of the low 32 bits of the weights
   u64 mhi[256];  // sums of the high 32 bits
 };
+
+struct WideLds {  // the finishing histogram: count and mass per bin
+  u32 cnt[kWide];
+  u64 mlo[kWide];
+  u64 mhi[kWide];
+};
+
+__device__ __forceinline__ Acc wide_bin(const WideLds& W, int b) {
+  return acc_of(mk128(W.mlo[b], 0) + ((u128)W.mhi[b] << 32), W.cnt[b]);
+}
+
+// Thread t holds the kWidePer bins kWide - 1 - (t * kWidePer + i), i.e. the
+// bins in descending order, with `ex` the (count, mass) of all bins before its
+// first and `mine` the sum of its own.  The bin where the running count (or,
+// by_mass, mass) first exceeds `target`: *bin (-1 if none), *before the
+// (count, mass) of the bins before it, *at its own.  All threads call it.
+__device__ __forceinline__ void wide_find(const WideLds& W, Acc ex, Acc mine, bool by_mass, u128 target, Scratch& sc,
+                                          int* bin, Acc* before, Acc* at) {
+  const int tid = threadIdx.x;
+  if (tid == 0) sc.i[1] = -1;
+  __syncthreads();
+  const u128 lo = by_mass ? acc_mass(ex) : (u128)ex.c;
+  const u128 sz = by_mass ? acc_mass(mine) : (u128)mine.c;
+  if (target >= lo && target < lo + sz) {
+    Acc run = ex;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+      const int b = kWide - 1 - (tid * kWidePer + i);
+      const Acc x = wide_bin(W, b);
+      const u128 hv = by_mass ? acc_mass(run) + acc_mass(x) : (u128)run.c + x.c;
+      if (!found && target < hv) {
+        found = true;
+        sc.i[1] = b;
+        sc.w[0] = run.lo;
+        sc.w[1] = run.hi;
+        sc.w[2] = run.c;
+        sc.w[3] = x.lo;
+        sc.w[4] = x.hi;
+        sc.w[5] = x.c;
+      }
+      if (!found) run = acc_add(run, x);
+    }
+  }
+  __syncthreads();
+  *bin = sc.i[1];
+  *before = Acc{uni64(sc.w[0]), uni64(sc.w[1]), uni((u32)sc.w[2])};
+  *at = Acc{uni64(sc.w[3]), uni64(sc.w[4]), uni((u32)sc.w[5])};
+  __syncthreads();
+}
 
 struct SelOut {
   u32 val;      // the selected 32-bit value
@@ -1199,13 +1252,15 @@ __device__ __forceinline__ void unpack_chunk(const Args& a, int row, int start, 
 // ---------------------------------------------------------------- region writes
 
 // Writes the chunk's tokens whose key kz is at least `thr` to the
-// workgroup's region as (key << 32 | id), in id order: the id start +
-// (v * 256 + t) * VW + j is ordered by (v, t, j).  Returns their number
-// (the same in every thread) and, in *below, the largest key under `thr`.
-// Nothing is written when they do not fit the region.
-template <int DT>
+// workgroup's region, in id order (the id start + (v * 256 + t) * VW + j is
+// ordered by (v, t, j)), as {id, key of q, M, n}: q = f_of_key(key) / T for
+// z keys (ZKEYS) or f_of_key(key) for q keys, and exp(q) = M * 2^(n - 23) as
+// in the weights.  Returns their number (the same in every thread) and, in
+// *below, the largest key under `thr`.  Nothing is written when they do not
+// fit the region.  The entries are read by k_finish, a later kernel.
+template <int DT, bool ZKEYS>
 __device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int start, int end, const u32 (&kz)[kEPT],
-                                           u32 thr, Scratch& sc, u32* below_out) {
+                                           u32 thr, float T, Scratch& sc, u32* below_out) {
   constexpr int VW = (DT == QS_DTYPE_F32) ? 4 : 8;
   constexpr int NV = kEPT / VW;
   constexpr int NW = (NV + 1) / 2;  // counts per vector packed two to a word (16-bit fields)
@@ -1253,7 +1308,7 @@ __device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int 
   for (int v = 0; v < NV; ++v) total += (tot[v >> 1] >> (16 * (v & 1))) & 0xffffu;
   *below_out = bmax;
   if (total > (u32)a.R) return total;
-  u64* rg = a.cand + ((size_t)row * a.G + blk) * a.R;
+  uint4* rg = a.cand + ((size_t)row * a.G + blk) * a.R;
   u32 run = 0u;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -1262,13 +1317,13 @@ __device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int 
     const u32 e0 = (u32)(start + (v * kThreads + tid) * VW);
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
-      const u32 k = kz[v * VW + j];
+      u32 k = kz[v * VW + j];
       if (k >= thr) {
-        // two 32-bit halves: a 64-bit entry would tie every key to the high
-        // half of a register pair
-        u32* ent = (u32*)&rg[pos];
-        stc(&ent[0], e0 + (u32)j);
-        stc(&ent[1], k);
+        asm volatile("" : "+v"(k));  // the entry is computed here, for written tokens only
+        const float q = ZKEYS ? f_of_key(k) / T : f_of_key(k);
+        const double y = y_of(q);
+        const double fl = floor(y);
+        rg[pos] = make_uint4(e0 + (u32)j, skey(q), mant24(exp2_poly((float)(y - fl))), (u32)(int)fl);
         ++pos;
       }
     }
@@ -1278,6 +1333,99 @@ __device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int 
 }
 
 // ---------------------------------------------------------------- finishing a row from its regions
+
+// finish_row with at most 256 merged candidates, in id order in LDS (ids,
+// keys, packed weights): one per thread.  Each candidate's rank in (q desc,
+// id asc) order is counted directly, the candidates are placed in that order,
+// and one prefix sum in it gives the top-k set, its mass and the top-p
+// boundary; a second, in id order, gives the draw.
+template <bool TOPK>
+__device__ __forceinline__ bool finish_small(const Args& a, const RowParams& p, int row, u32 m, int N, u32 nout,
+                                             unsigned char* lds, Scratch& sc) {
+  const int tid = threadIdx.x;
+  u32* st_id = (u32*)lds;
+  u32* st_key = st_id + kFinCap;
+  u32* st_wp = st_key + kFinCap;
+  const bool have = (u32)tid < m;
+  const u32 mkey = have ? st_key[tid] : 0u, mid = have ? st_id[tid] : 0u, mwp = have ? st_wp[tid] : 0u;
+  // rank: members with a larger key, or the same key and a smaller id (an earlier slot)
+  u32 rank = 0u;
+  if (have) {
+    u32 j = 0u;
+    for (; j + 4u <= m; j += 4u) {
+      const uint4 k4 = *(const uint4*)&st_key[j];
+      rank += (k4.x > mkey || (k4.x == mkey && j < (u32)tid)) ? 1u : 0u;
+      rank += (k4.y > mkey || (k4.y == mkey && j + 1u < (u32)tid)) ? 1u : 0u;
+      rank += (k4.z > mkey || (k4.z == mkey && j + 2u < (u32)tid)) ? 1u : 0u;
+      rank += (k4.w > mkey || (k4.w == mkey && j + 3u < (u32)tid)) ? 1u : 0u;
+    }
+    for (; j < m; ++j) {
+      const u32 kj = st_key[j];
+      rank += (kj > mkey || (kj == mkey && j < (u32)tid)) ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+  if (have) {
+    st_key[rank] = mkey;
+    st_wp[rank] = mwp;
+    st_id[rank] = mid;
+  }
+  __syncthreads();
+  // thread i now holds the candidate of rank i
+  const u32 rkey = have ? st_key[tid] : 0u, rwp = have ? st_wp[tid] : 0u, rid = have ? st_id[tid] : 0u;
+  u32 kappa = 0u;
+  if (TOPK) {
+    if (m < (u32)p.k) return give_up(a, row, kWhyFewer);
+    kappa = st_key[p.k - 1];
+    // every token left out has a q key <= nout: it must be below the k-th
+    if (nout > 0u && nout >= kappa) return give_up(a, row, kWhyIncomplete);
+  }
+  QS_TR(6);
+  const bool intop = have && rkey >= kappa;
+  const u128 rw = intop ? (u128)wunpack(rwp) : (u128)0;
+  Acc tot;
+  const Acc ex = block_scan_acc(acc_of(rw, intop ? 1u : 0u), sc, &tot);
+  const u128 S = acc_mass(tot);
+  QS_TR(13);
+  u32 kp = kappa, idp = 0xffffffffu;  // kept: key > kp || (key == kp && id <= idp)
+  u128 W = S;
+  if (p.topp_on) {
+    // the first candidate in this order whose inclusive mass exceeds floor(top_p * S)
+    const u128 Tp = mul_frac(S, p.tp);
+    if (tid == 0) sc.r[5] = 0xffffffffu;
+    __syncthreads();
+    if (intop && Tp >= acc_mass(ex) && Tp < acc_mass(ex) + rw) {
+      sc.r[5] = (u32)tid;
+      sc.w[6] = (u64)(acc_mass(ex) + rw);
+      sc.w[7] = (u64)((acc_mass(ex) + rw) >> 64);
+    }
+    __syncthreads();
+    const u32 c = sc.r[5];
+    if (c == 0xffffffffu) return give_up(a, row, kWhyTopP);
+    kp = st_key[c];
+    idp = st_id[c];
+    W = mk128(sc.w[6], sc.w[7]);
+    __syncthreads();
+  }
+  QS_TR(7);
+  // ---- the draw: kept candidates in id order, which is the order of the slots
+  const u128 t = mul_frac(W, p.u);
+  const bool kept = have && (mkey > kp || (mkey == kp && mid <= idp));
+  const u128 mw = kept ? (u128)wunpack(mwp) : (u128)0;
+  if (tid == 0) sc.r[6] = 0xffffffffu;
+  const Acc dx = block_scan_acc(acc_of(mw, 0u), sc, &tot);
+  if (kept && t >= acc_mass(dx) && t < acc_mass(dx) + mw) sc.r[6] = mid;
+  __syncthreads();
+  const u32 chosen = sc.r[6];
+  __syncthreads();
+  QS_TR(9);
+  (void)rid;
+  if (tid == 0)
+    publish_result(a, row, chosen == 0xffffffffu ? -1ll : (long long)chosen, N, W, kp, idp, false, TOPK ? 1u : 4u);
+  __syncthreads();
+  return true;
+}
+
 
 // Resolves a row from the regions of all its workgroups: the last workgroup of
 // a top-k row (TOPK: entries hold z keys; k-select, then a proof that no token
@@ -1291,42 +1439,66 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
                                            Scratch& sc) {
   const int tid = threadIdx.x;
   const Slot* sl = a.slots + (size_t)row * a.G;
-  const u64* cd = a.cand + (size_t)row * a.G * a.R;
-  const int total = a.G * a.R;  // <= kRegionTotal, a multiple of kGatherPer
-  const int f0 = tid * kGatherPer;
-  const bool have = f0 < total;
-  const int g = f0 >> a.logR;
-  const u32 s0 = (u32)(f0 & (a.R - 1));
-  // ---- gather: this thread's kGatherPer region entries and their region's header
-  u64 ent[kGatherPer];
+  const uint4* cd = a.cand + (size_t)row * a.G * a.R;
+  // (written by k_sample, an earlier kernel on this stream: plain loads see it)
+  // ---- the regions' headers: one region per thread (G <= 256)
+  u32* hoff = (u32*)lds;  // [kMaxChunks + 1] start of each region's entries in the concatenation
   u32 cnt = 0u, tau = 0u, below = 0u;
-  if (have) {
-    cnt = ldc(&sl[g].nb);
+  if (tid < a.G) {
+    cnt = sl[tid].nb;
     if (TOPK) {
-      tau = ldc(&sl[g].tau);
-      below = ldc(&sl[g].below);
+      tau = sl[tid].tau;
+      below = sl[tid].below;
     }
-#pragma unroll
-    for (int q = 0; q < kGatherPer; ++q) ent[q] = ldc(&cd[f0 + q]);
-  } else {
-#pragma unroll
-    for (int q = 0; q < kGatherPer; ++q) ent[q] = 0ull;
   }
-  u32 ovf = (have && cnt == 0xffffffffu) ? 1u : 0u;
+  u32 ovf = cnt == 0xffffffffu ? 1u : 0u;
+  if (ovf) cnt = 0u;
+  u32 m0;
+  const u32 coff = block_scan_u32(cnt, sc, &m0);
   u32 tstar = tau;
-  block_max3(tstar, ovf, below, sc);
+  block_max3(tstar, ovf, below, sc);  // its barriers also order hoff below
+  if (tid < a.G) hoff[tid] = coff;
+  if (tid == 0) hoff[a.G] = m0;
+  __syncthreads();
   QS_TR(11);
   if (ovf) return give_up(a, row, kWhyRegion);
-  // ---- entries at or above the threshold, compacted in id order through LDS
-  const u32 thr = TOPK ? tstar : kthr;
-  u32 flags = 0u, npass = 0u, dropmax = 0u;
+  if (m0 > (u32)(kThreads * kGatherPer)) return give_up(a, row, kWhyMerge);
+  // ---- this thread's share of the concatenated entries (id order): flat
+  // indices [f0, f0 + per); all loads issued before any is used
+  const u32 per = (m0 + kThreads - 1) / kThreads;  // <= kGatherPer
+  const u32 f0 = (u32)tid * per;
+  int g = 0;
+  if (f0 < m0) {
+    int lo = 0, hi = a.G - 1;  // the last region starting at or before f0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (hoff[mid] <= f0) lo = mid; else hi = mid - 1;
+    }
+    g = lo;
+  }
+  uint4 ent[kGatherPer];
 #pragma unroll
   for (int q = 0; q < kGatherPer; ++q) {
-    if (have && s0 + (u32)q < cnt) {
-      const u32 k = (u32)(ent[q] >> 32);
+    const u32 f = f0 + (u32)q;
+    ent[q] = make_uint4(0u, 0u, 0u, 0u);
+    if ((u32)q < per && f < m0) {
+      while (hoff[g + 1] <= f) ++g;
+      ent[q] = cd[(size_t)g * a.R + (f - hoff[g])];
+    }
+  }
+  // ---- entries at or above the threshold, compacted in id order through LDS;
+  // the weights need the row scale N = the largest octave among them
+  const u32 thr = TOPK ? skey(f_of_key(tstar) / p.T) : kthr;
+  u32 flags = 0u, npass = 0u, dropmax = 0u;
+  int nmax = (int)0x80000000u;
+#pragma unroll
+  for (int q = 0; q < kGatherPer; ++q) {
+    if ((u32)q < per && f0 + (u32)q < m0) {
+      const u32 k = ent[q].y;
       if (k >= thr) {
         flags |= 1u << q;
         ++npass;
+        nmax = (int)ent[q].w > nmax ? (int)ent[q].w : nmax;
       } else {
         dropmax = k > dropmax ? k : dropmax;
       }
@@ -1334,89 +1506,197 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
   }
   u32 m;
   const u32 off = block_scan_u32(npass, sc, &m);
-  u32 nout = 0u;
-  if (TOPK) nout = block_max_u32(dropmax > below ? dropmax : below, sc);
+  u32 nout = 0u, nmx = (u32)nmax ^ 0x80000000u, dummy = 0u;
+  if (TOPK) {
+    // largest q key of the tokens left out: dropped entries, and below each region's threshold
+    const u32 bq = below ? skey(f_of_key(below) / p.T) : 0u;
+    nout = dropmax > bq ? dropmax : bq;
+  }
+  block_max3(nout, nmx, dummy, sc);
+  const int N = (int)(nmx ^ 0x80000000u);
   if (m > (u32)kFinCap) return give_up(a, row, kWhyMerge);
   if (TOPK && m < (u32)p.k) return give_up(a, row, kWhyFewer);
-  u64* stage = (u64*)lds;
+  u32* st_id = (u32*)lds;
+  u32* st_key = st_id + kFinCap;
+  u32* st_wp = st_key + kFinCap;
   {
     u32 pos = off;
 #pragma unroll
-    for (int q = 0; q < kGatherPer; ++q)
-      if ((flags >> q) & 1u) stage[pos++] = ent[q];
+    for (int q = 0; q < kGatherPer; ++q) {
+      if ((flags >> q) & 1u) {
+        const int r = (int)ent[q].w - N + kWindow;
+        st_id[pos] = ent[q].x;
+        st_key[pos] = ent[q].y;
+        st_wp[pos] = r >= 0 ? ((u32)r << 24) | ent[q].z : 0u;
+        ++pos;
+      }
+    }
   }
   __syncthreads();
+  if (m <= (u32)kThreads) return finish_small<TOPK>(a, p, row, m, N, nout, lds, sc);
   u32 key[kFinPer], id[kFinPer], wp[kFinPer], memb = 0u;
+  u32 kmx = 0u;
 #pragma unroll
   for (int j = 0; j < kFinPer; ++j) {
     const u32 i = (u32)(tid * kFinPer + j);
     if (i < m) {
-      const u64 e = stage[i];
-      key[j] = (u32)(e >> 32);
-      id[j] = (u32)e;
+      key[j] = st_key[i];
+      id[j] = st_id[i];
+      wp[j] = st_wp[i];
       memb |= 1u << j;
+      kmx = key[j] > kmx ? key[j] : kmx;
     } else {
       key[j] = 0u;
       id[j] = 0u;
+      wp[j] = 0u;
     }
   }
-  __syncthreads();  // the staging area becomes the select buffers
+  __syncthreads();  // the staging area becomes the histogram and select buffers
   QS_TR(5);
-  // ---- q keys, the row scale, packed weights
-  u32 kmx = 0u;
+  // ---- one histogram of the members over 11 bits of the key (count and mass
+  // per bin), scanned once from the top; the bins holding the k-th key and the
+  // top-p boundary are then resolved among their own members only
+  WideLds& WL = *(WideLds*)lds;
+  SelLds* SL = (SelLds*)(lds + sizeof(WideLds));
+  u32 nkmn = 0u, anym = memb ? 1u : 0u, kmx2 = kmx;
+#pragma unroll
+  for (int j = 0; j < kFinPer; ++j)
+    if ((memb >> j) & 1u) nkmn = ~key[j] > nkmn ? ~key[j] : nkmn;
+  block_max3(nkmn, anym, kmx2, sc);
+  if (!anym) return give_up(a, row, kWhyKSelect);
+  const u32 kfirst = uni(~nkmn), kdiff = uni(kmx2) ^ kfirst;
+  const int hib = kdiff ? 31 - __clz(kdiff) : 0;
+  const int lob = hib >= kWideBits - 1 ? hib - (kWideBits - 1) : 0;
+  // bits above hib are common to all members, so the digit is monotone in the key;
+  // with lob == 0 a bin holds a single key, (kfirst & ~(kWide - 1)) | bin
+  for (int i = tid; i < kWide; i += kThreads) {
+    WL.cnt[i] = 0u;
+    WL.mlo[i] = 0ull;
+    WL.mhi[i] = 0ull;
+  }
+  __syncthreads();
 #pragma unroll
   for (int j = 0; j < kFinPer; ++j) {
     if ((memb >> j) & 1u) {
-      if (TOPK) key[j] = skey(f_of_key(key[j]) / p.T);
-      kmx = key[j] > kmx ? key[j] : kmx;
+      const u32 d = (key[j] >> lob) & (u32)(kWide - 1);
+      atomicAdd(&WL.cnt[d], 1u);
+      u32 wj = wp[j];
+      asm volatile("" : "+v"(wj));
+      const u64 w = wunpack(wj);
+      if (w) {
+        atomicAdd(&WL.mlo[d], w & 0xffffffffull);
+        atomicAdd(&WL.mhi[d], w >> 32);
+      }
     }
   }
-  kmx = block_max_u32(kmx, sc);
-  const int N = octave_of(f_of_key(kmx));
+  __syncthreads();
+  Acc wmine = {0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < kFinPer; ++j) wp[j] = ((memb >> j) & 1u) ? wpack(f_of_key(key[j]), N) : 0u;
-  SelLds* SL = (SelLds*)lds;
+  for (int i = 0; i < kWidePer; ++i) wmine = acc_add(wmine, wide_bin(WL, kWide - 1 - (tid * kWidePer + i)));
+  Acc wtot;
+  const Acc wex = block_scan_acc(wmine, sc, &wtot);
+  auto digit = [&](u32 k) { return (int)((k >> lob) & (u32)(kWide - 1)); };
   // ---- top-k: the k-th largest q, and the proof that the candidates hold the top-k set
   u32 kappa = 0u;
+  int bk = -1;
+  Acc kb = {0, 0, 0}, ka = {0, 0, 0};  // bins above kappa's, kappa's bin
   if (TOPK) {
-    const SelOut sk = reg_select<false>(key, memb, wp, (u128)(p.k - 1), SL, sc);
-    if (!sk.ok) return give_up(a, row, kWhyKSelect);
-    kappa = sk.val;
-    QS_TR(6);
-    // every token left out has z <= f_of_key(nout), so q <= that / T: it must be below the k-th
-    if (nout > 0u && skey(f_of_key(nout) / p.T) >= kappa) return give_up(a, row, kWhyIncomplete);
-  }
-  u32 intop = 0u;
-  u128 sv = 0;
+    wide_find(WL, wex, wmine, false, (u128)(p.k - 1), sc, &bk, &kb, &ka);
+    if (bk < 0) return give_up(a, row, kWhyKSelect);
+    if (lob == 0) {
+      kappa = (kfirst & ~(u32)(kWide - 1)) | (u32)bk;
+    } else {
+      u32 mk = 0u, bmx = 0u, bnmn = 0u, dummy = 0u;
 #pragma unroll
-  for (int j = 0; j < kFinPer; ++j) {
-    if (((memb >> j) & 1u) && key[j] >= kappa) {
-      intop |= 1u << j;
-      sv += (u128)wunpack(wp[j]);
+      for (int j = 0; j < kFinPer; ++j) {
+        if (((memb >> j) & 1u) && digit(key[j]) == bk) {
+          mk |= 1u << j;
+          bmx = key[j] > bmx ? key[j] : bmx;
+          bnmn = ~key[j] > bnmn ? ~key[j] : bnmn;
+        }
+      }
+      block_max3(bmx, bnmn, dummy, sc);
+      if (bmx == ~bnmn) {
+        kappa = bmx;  // the bin holds a single key
+      } else {
+        const SelOut sk = reg_select<false>(key, mk, wp, (u128)(p.k - 1 - kb.c), SL, sc);
+        if (!sk.ok) return give_up(a, row, kWhyKSelect);
+        kappa = sk.val;
+      }
     }
+    QS_TR(6);
+    // every token left out has a q key <= nout: it must be below the k-th
+    if (nout > 0u && nout >= kappa) return give_up(a, row, kWhyIncomplete);
   }
-  const u128 S = block_sum128(sv, sc);
+  u128 S;
+  if (TOPK) {
+    u128 sv = 0;
+#pragma unroll
+    for (int j = 0; j < kFinPer; ++j)
+      if (((memb >> j) & 1u) && key[j] >= kappa) sv += (u128)wunpack(wp[j]);
+    S = uni128(block_sum128(sv, sc));
+  } else {
+    S = acc_mass(wtot);
+  }
   QS_TR(13);
   u32 kp = kappa, idp = 0xffffffffu;  // kept: key > kp || (key == kp && id <= idp)
   u128 W = S;
   if (p.topp_on) {
     // the first token (q desc, id asc) whose inclusive mass exceeds floor(top_p * S)
-    const u128 Tp = mul_frac(S, p.tp);
-    const SelOut sp = reg_select<true>(key, intop, wp, Tp, SL, sc);
+    const u128 Tp = uni128(mul_frac(S, p.tp));
+    int bp;
+    Acc pb, pa;
+    bool restrict_k = false;  // the boundary lies in kappa's bin, among its keys >= kappa
+    if (TOPK && Tp >= acc_mass(kb)) {
+      bp = bk;
+      pb = kb;
+      pa = ka;
+      restrict_k = true;
+    } else {
+      wide_find(WL, wex, wmine, true, Tp, sc, &bp, &pb, &pa);
+      if (bp < 0) return give_up(a, row, kWhyTopP);
+    }
+    u128 A;
+    Acc at;
+    if (lob == 0) {
+      kp = (kfirst & ~(u32)(kWide - 1)) | (u32)bp;
+      A = acc_mass(pb);
+      at = pa;
+    } else {
+      u32 mp = 0u, bmx = 0u, bnmn = 0u, dummy = 0u;
+#pragma unroll
+      for (int j = 0; j < kFinPer; ++j) {
+        if (((memb >> j) & 1u) && digit(key[j]) == bp && (!restrict_k || key[j] >= kappa)) {
+          mp |= 1u << j;
+          bmx = key[j] > bmx ? key[j] : bmx;
+          bnmn = ~key[j] > bnmn ? ~key[j] : bnmn;
+        }
+      }
+      block_max3(bmx, bnmn, dummy, sc);
+      if (!restrict_k && bmx == ~bnmn) {
+        // the bin holds a single key
+        kp = bmx;
+        A = acc_mass(pb);
+        at = pa;
+      } else {
+        const SelOut sp = reg_select<true>(key, mp, wp, Tp - acc_mass(pb), SL, sc);
+        if (!sp.ok) return give_up(a, row, kWhyTopP);
+        kp = sp.val;
+        A = acc_mass(pb) + acc_mass(sp.before);
+        at = sp.at;
+      }
+    }
     QS_TR(14);
-    if (!sp.ok) return give_up(a, row, kWhyTopP);
-    kp = sp.val;
-    const u128 A = acc_mass(sp.before);
     const u64 wk = wunpack(wpack(f_of_key(kp), N));
-    const u64 jb = div_small(Tp - A, wk);  // 0-based boundary member among the ties (< sp.at.c)
-    if (jb + 1 >= sp.at.c) {
-      W = A + acc_mass(sp.at);
+    const u64 jb = div_small(Tp - A, wk);  // 0-based boundary member among the ties (< at.c)
+    if (jb + 1 >= at.c) {
+      W = A + acc_mass(at);
     } else {
       W = A + (u128)wk * (u128)(jb + 1);
       // the boundary member: tie member jb in id order, which is register order
       u32 c = 0u;
 #pragma unroll
-      for (int j = 0; j < kFinPer; ++j) c += (((intop >> j) & 1u) && key[j] == kp) ? 1u : 0u;
+      for (int j = 0; j < kFinPer; ++j) c += (((memb >> j) & 1u) && key[j] == kp) ? 1u : 0u;
       if (tid == 0) sc.r[5] = 0xffffffffu;
       u32 ct;
       const u32 ex = block_scan_u32(c, sc, &ct);
@@ -1424,7 +1704,7 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
         u32 r = ex;
 #pragma unroll
         for (int j = 0; j < kFinPer; ++j) {
-          if (((intop >> j) & 1u) && key[j] == kp) {
+          if (((memb >> j) & 1u) && key[j] == kp) {
             if (r == (u32)jb) sc.r[5] = id[j];
             ++r;
           }
@@ -1804,17 +2084,32 @@ __device__ __forceinline__ void load_chunk_pen(const Args& a, const RowParams& p
   // registers, so they are loaded after it
   if (DT == QS_DTYPE_BF16) issue_chunk<DT>(a, row, start, end, cl);
   if (p.pen_on) pen_build(a, row, start, end, pt, sc);
+  QS_TR(8);
   if (DT == QS_DTYPE_F32) issue_chunk<DT>(a, row, start, end, cl);
   unpack_chunk<DT>(a, row, start, end, cl, z);
+  QS_TR(9);
   if (p.pen_on) {
+    // one bitmap word per vector (its VW tokens are aligned inside one word);
+    // counts are looked up only for the tokens present in the history
+    u32 pres[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
+      const int o = (v * kThreads + tid) * VW;  // chunk-relative
+      pres[v] = o < end - start ? (pt.bits[o >> 5] >> (o & 31)) & ((1u << VW) - 1u) : 0u;
+    }
 #pragma unroll
-      for (int j = 0; j < VW; ++j) {
-        const int e = start + (v * kThreads + tid) * VW + j;
-        if (e < end) {
-          const u32 cnt = pen_count(pt, e - start);
-          if (cnt) z[v * VW + j] = apply_penalty(z[v * VW + j], cnt, p.rep, p.pres, p.freq);
+    for (int v = 0; v < NV; ++v) {
+      if (pres[v]) {  // rare: a vector with a history token
+        const int o = (v * kThreads + tid) * VW;
+        const u32 bw = pt.bits[o >> 5];
+        const u32 base = pt.wpre[o >> 5];
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          if ((pres[v] >> j) & 1u) {
+            const int l = o + j;
+            const u32 cnt = pt.cnts[base + __popc(bw & ((1u << (l & 31)) - 1u))];
+            z[v * VW + j] = apply_penalty(z[v * VW + j], cnt, p.rep, p.pres, p.freq);
+          }
         }
       }
     }
@@ -1919,7 +2214,12 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
     u32 tau = sc.v[0][6];
     for (int w = 1; w < kWaves; ++w) tau = sc.v[w][6] < tau ? sc.v[w][6] : tau;
     u32 below;
-    const u32 total = emit_region<DT>(a, row, blk, start, end, kz, tau, sc, &below);
+    u32 total = emit_region<DT, true>(a, row, blk, start, end, kz, tau, p.T, sc, &below);
+    if (total > (u32)a.R) {
+      // too many tokens at the threshold (ties): leave those at tau out
+      if (tau != 0xffffffffu) ++tau;
+      total = emit_region<DT, true>(a, row, blk, start, end, kz, tau, p.T, sc, &below);
+    }
     if (tid == 0) {
       Slot* sl = a.slots + (size_t)row * a.G + blk;
       stc(&sl->nb, total <= (u32)a.R ? total : 0xffffffffu);
@@ -1949,7 +2249,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
     block_max3(kmx, nkmn, dummy, sc);
     const u32 kthr_l = window_key(octave_of(f_of_key(kmx)) - kWindow);
     u32 below;
-    const u32 total = emit_region<DT>(a, row, blk, start, end, kz, kthr_l, sc, &below);
+    const u32 total = emit_region<DT, false>(a, row, blk, start, end, kz, kthr_l, 1.0f, sc, &below);
     QS_TR(2);
     if (tid == 0) {
       const bool fits = total <= (u32)a.R;
@@ -2116,6 +2416,9 @@ __global__ __launch_bounds__(kThreads) void k_finish(Args a) {
   if (ROLE == 0) {
     if (p.kind == kGreedy || (p.kind == kMass && !(a.flags & QS_FLAG_NO_MASS_ROWS))) return;
     QS_TR(0);
+#ifdef QS_TRACE
+    if (a.trace && threadIdx.x == 0) a.trace[(size_t)sc.tslot * 16 + 1] = clock64();
+#endif
     if (p.kind == kTopK) {
       if (!finish_row<true>(a, p, row, 0u, lds, sc)) resolve_single<DT>(a, p, row, lds, sc);
     } else {
@@ -2124,6 +2427,9 @@ __global__ __launch_bounds__(kThreads) void k_finish(Args a) {
     }
     reset_row(a, row);
     QS_TR(15);
+#ifdef QS_TRACE
+    if (a.trace && threadIdx.x == 0) a.trace[(size_t)sc.tslot * 16 + 2] = clock64();
+#endif
     return;
   }
   if (p.kind != kMass) return;
@@ -2244,7 +2550,7 @@ Layout layout_for(int B, int V, int H) {
   L.off_ctl = o;
   o = align_up(o + (size_t)B * sizeof(RowCtl), 256);
   L.off_cand = o;
-  o = align_up(o + (size_t)B * L.G * L.R * 8, 256);
+  o = align_up(o + (size_t)B * L.G * L.R * 16, 256);
   L.off_hist = o;
   o = align_up(o + (size_t)B * kBins * 8, 256);
   L.off_list = o;
@@ -2253,7 +2559,8 @@ Layout layout_for(int B, int V, int H) {
   o = align_up(o + (size_t)B * L.G * sizeof(Slot), 256);
   L.total = o;
   const size_t pen = H > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 0;
-  const size_t fin = (size_t)kFinCap * 8;  // staging, then 2 * SelLds
+  const size_t stage = (size_t)3 * kFinCap * 4;  // finish_row's staging: ids, keys, weights
+  const size_t fin = stage > sizeof(WideLds) + 2 * sizeof(SelLds) ? stage : sizeof(WideLds) + 2 * sizeof(SelLds);
   const size_t flat = sizeof(FlatLds);
   const size_t single = sizeof(SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
   const size_t bins = (size_t)3 * kBins * 8 + (size_t)3 * kHash * 4;  // flat mass rows in k_sample
@@ -2264,7 +2571,6 @@ Layout layout_for(int B, int V, int H) {
   if (single > L.lds_finish) L.lds_finish = single;
   return L;
 }
-static_assert(2 * sizeof(SelLds) <= (size_t)kFinCap * 8, "select buffers fit the staging area");
 
 // k_sample then, unless every row is greedy, k_finish, on one stream.
 template <int DT, int ROLE>
@@ -2358,7 +2664,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   a.out_kept = out_kept;
   char* base = (char*)ws;
   a.ctl = (RowCtl*)(base + L.off_ctl);
-  a.cand = (u64*)(base + L.off_cand);
+  a.cand = (uint4*)(base + L.off_cand);
   a.mhist = (u64*)(base + L.off_hist);
   a.list = (u64*)(base + L.off_list);
   a.slots = (Slot*)(base + L.off_slots);
