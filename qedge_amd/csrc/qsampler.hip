@@ -60,6 +60,8 @@ constexpr double kLog2e = 1.4426950408889634074;
 constexpr int kTopkFast = QS_TOPK_FAST_MAX;
 constexpr int kGatherPer = 16;                    // region entries one finishing thread loads
 constexpr int kRegionTotal = 8192;                // G * R <= this (the entries written stay <= kThreads * kGatherPer)
+constexpr int kStageCap = 1024;
+constexpr int kHoffBytes = 2048;                  // finish_row: region offsets ahead of the histogram                   // region entries staged in LDS by one workgroup
 constexpr int kFinPer = 16;                       // merged candidates per thread
 constexpr int kFinCap = kThreads * kFinPer;       // merged candidates per row
 constexpr int kBins = 256;                        // histogram bins
@@ -67,7 +69,10 @@ constexpr int kWideBits = 11;                     // finishing histogram: 2048 b
 constexpr int kWide = 1 << kWideBits;
 constexpr int kWidePer = kWide / kThreads;        // bins per thread
 constexpr int kListCap = kFinCap;                 // bracket entries per row (flat mass rows)
-constexpr int kHash = 1024;                       // bracketed tokens per chunk (flat mass rows)
+constexpr int kHash = 1024;
+constexpr int kStage2 = 2048;                      // bracketed tokens staged per chunk (flat mass rows)
+constexpr int kSegEnt = 512;                      // (key, segment) entries per chunk (flat mass rows)
+constexpr int kSegs = 32;                          // segments per chunk (vector x wave), at most                       // bracketed tokens per chunk (flat mass rows)
 constexpr int kMaxChunks = 256;                   // chunks per row (G)
 constexpr int kMaxHistory = QS_MAX_HISTORY;
 constexpr u32 kSpinLimit = 1u << 21;
@@ -126,7 +131,8 @@ struct __attribute__((aligned(64))) Slot {
   u32 tau;         // top-k rows: the region's threshold (z key)
   u32 below;       // top-k rows: largest z key below tau in the chunk
   u32 nbr;         // flat mass rows: bracketed tokens of the chunk
-  u32 pad[4];
+  u32 nse;         // flat mass rows: (key, segment) entries of the chunk (0xffffffff: more than fit)
+  u32 pad[3];
 };
 static_assert(sizeof(Slot) == 64, "slot is 64 bytes");
 
@@ -150,6 +156,8 @@ struct Args {
   uint4* cand; // [B, G, R] region entries {id, q key, exp2 mantissa M, octave n}
   u64* mhist;  // [B, kBins] global mass histogram (flat mass rows)
   u64* list;   // [B, kListCap] bracket entries (key << 32 | chunk << 16 | count), flat mass rows
+  u64* sent;   // [B, G, kSegEnt] per chunk: bracket entries (key << 32 | segment << 16 | count), flat mass rows
+  u64* segm;   // [B, G, kSegs, 2] flat mass rows: exact mass per segment (above the bracket with top-p), lo, hi
   Slot* slots; // [B, G]
   u64* trace;  // per-workgroup phase timestamps (trace builds only)
 };
@@ -358,7 +366,8 @@ __device__ __forceinline__ RowParams row_params(const Args& a, int row) {
 
 struct Scratch {   // static LDS
   u64 w[20];              // [12, 15]: find_bin results; [8, 20): select results
-  u32 u[8];
+  u64 fw[12];             // wide_find results: [0, 6) slot 0, [6, 12) slot 1
+  u32 u[8];               // finish_row: key range of a bin
   u32 v[kWaves][8];       // per-wave partials of the block collectives
   int i[8];               // find_bin
   u32 r[16];              // results and counters of the callers
@@ -391,6 +400,16 @@ __device__ __forceinline__ u32 wave_max(u32 v) {
   v = max(v, dpp_mov<0x142, 0xA>(v));  // row_bcast:15
   v = max(v, dpp_mov<0x143, 0xC>(v));  // row_bcast:31
   return (u32)__builtin_amdgcn_readlane((int)v, 63);
+}
+// Sum over the wave, returned to every lane.
+__device__ __forceinline__ u32 wave_sum(u32 v) { return (u32)__builtin_amdgcn_readlane((int)wave_incl_scan(v), 63); }
+// Exact sum over the wave of lo + hi * 2^64 (hi < 2^22), in 22-bit limbs.
+__device__ __forceinline__ u128 wave_sum128(u64 lo, u32 hi) {
+  const u32 l0 = wave_sum((u32)lo & 0x3fffffu);
+  const u32 l1 = wave_sum((u32)(lo >> 22) & 0x3fffffu);
+  const u32 l2 = wave_sum((u32)(lo >> 44));
+  const u32 l3 = wave_sum(hi);
+  return (u128)l0 + ((u128)l1 << 22) + ((u128)l2 << 44) + ((u128)l3 << 64);
 }
 template <int CTRL, int ROWMASK>
 __device__ __forceinline__ void max64_step(u32& hi, u32& lo) {
@@ -462,6 +481,37 @@ __device__ __forceinline__ u32 block_scan_u32(u32 v, Scratch& s, u32* total) {
     const u32 x = s.v[i][0];
     base += (i < wv) ? x : 0u;
     tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + inc - v;
+}
+
+// Exclusive scan of v in thread order (total in *total) and the maxima of
+// x[0..NX) over the workgroup (returned in x): one LDS exchange.
+template <int NX>
+__device__ __forceinline__ u32 block_scan_max(u32 v, u32 (&x)[NX], Scratch& s, u32* total) {
+  static_assert(NX <= 7, "per-wave slots");
+  const int wv = threadIdx.x >> 6;
+  const u32 inc = wave_incl_scan(v);
+  u32 mx[NX];
+#pragma unroll
+  for (int i = 0; i < NX; ++i) mx[i] = wave_max(x[i]);
+  if (lane_id() == 63) s.v[wv][0] = inc;
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) s.v[wv][1 + i] = mx[i];
+  }
+  __syncthreads();
+  u32 base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < NX; ++i) x[i] = 0u;
+  for (int w = 0; w < kWaves; ++w) {
+    const u32 c = s.v[w][0];
+    base += (w < wv) ? c : 0u;
+    tot += c;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) x[i] = s.v[w][1 + i] > x[i] ? s.v[w][1 + i] : x[i];
   }
   __syncthreads();
   *total = tot;
@@ -596,43 +646,40 @@ __device__ __forceinline__ Acc wide_bin(const WideLds& W, int b) {
 }
 
 // Thread t holds the kWidePer bins kWide - 1 - (t * kWidePer + i), i.e. the
-// bins in descending order, with `ex` the (count, mass) of all bins before its
-// first and `mine` the sum of its own.  The bin where the running count (or,
-// by_mass, mass) first exceeds `target`: *bin (-1 if none), *before the
-// (count, mass) of the bins before it, *at its own.  All threads call it.
-__device__ __forceinline__ void wide_find(const WideLds& W, Acc ex, Acc mine, bool by_mass, u128 target, Scratch& sc,
-                                          int* bin, Acc* before, Acc* at) {
+// bins in descending order: bin[i] their (count, mass), `ex` the sum of all
+// bins before its first.  The bin where the running count (or, by_mass, mass)
+// first exceeds `target`: *bin (-1 if none), *before the (count, mass) of the
+// bins before it, *at its own.  Result slot `slot` (0 or 1): the caller has set
+// sc.i[1 + slot] = -1 before a barrier that every thread has passed since.
+// All threads call it.
+__device__ __forceinline__ void wide_find(const Acc (&bin)[kWidePer], Acc ex, bool by_mass, u128 target, Scratch& sc,
+                                          int slot, int* bout, Acc* before, Acc* at) {
   const int tid = threadIdx.x;
-  if (tid == 0) sc.i[1] = -1;
-  __syncthreads();
-  const u128 lo = by_mass ? acc_mass(ex) : (u128)ex.c;
-  const u128 sz = by_mass ? acc_mass(mine) : (u128)mine.c;
-  if (target >= lo && target < lo + sz) {
-    Acc run = ex;
-    bool found = false;
+  Acc run = ex;
+  bool found = false;
 #pragma unroll
-    for (int i = 0; i < kWidePer; ++i) {
-      const int b = kWide - 1 - (tid * kWidePer + i);
-      const Acc x = wide_bin(W, b);
-      const u128 hv = by_mass ? acc_mass(run) + acc_mass(x) : (u128)run.c + x.c;
-      if (!found && target < hv) {
-        found = true;
-        sc.i[1] = b;
-        sc.w[0] = run.lo;
-        sc.w[1] = run.hi;
-        sc.w[2] = run.c;
-        sc.w[3] = x.lo;
-        sc.w[4] = x.hi;
-        sc.w[5] = x.c;
-      }
-      if (!found) run = acc_add(run, x);
+  for (int i = 0; i < kWidePer; ++i) {
+    const Acc x = bin[i];
+    const u128 lo = by_mass ? acc_mass(run) : (u128)run.c;
+    const u128 sz = by_mass ? acc_mass(x) : (u128)x.c;
+    if (!found && sz > 0 && target >= lo && target < lo + sz) {
+      found = true;
+      sc.i[1 + slot] = kWide - 1 - (tid * kWidePer + i);
+      u64* f = sc.fw + 6 * slot;
+      f[0] = run.lo;
+      f[1] = run.hi;
+      f[2] = run.c;
+      f[3] = x.lo;
+      f[4] = x.hi;
+      f[5] = x.c;
     }
+    run = acc_add(run, x);
   }
   __syncthreads();
-  *bin = sc.i[1];
-  *before = Acc{uni64(sc.w[0]), uni64(sc.w[1]), uni((u32)sc.w[2])};
-  *at = Acc{uni64(sc.w[3]), uni64(sc.w[4]), uni((u32)sc.w[5])};
-  __syncthreads();
+  const u64* f = sc.fw + 6 * slot;
+  *bout = sc.i[1 + slot];
+  *before = Acc{uni64(f[0]), uni64(f[1]), uni((u32)f[2])};
+  *at = Acc{uni64(f[3]), uni64(f[4]), uni((u32)f[5])};
 }
 
 struct SelOut {
@@ -1255,12 +1302,15 @@ __device__ __forceinline__ void unpack_chunk(const Args& a, int row, int start, 
 // workgroup's region, in id order (the id start + (v * 256 + t) * VW + j is
 // ordered by (v, t, j)), as {id, key of q, M, n}: q = f_of_key(key) / T for
 // z keys (ZKEYS) or f_of_key(key) for q keys, and exp(q) = M * 2^(n - 23) as
-// in the weights.  Returns their number (the same in every thread) and, in
-// *below, the largest key under `thr`.  Nothing is written when they do not
-// fit the region.  The entries are read by k_finish, a later kernel.
+// in the weights.  The tokens are first staged in LDS as (chunk index, key) at
+// their final positions; the entries are then computed one per thread and
+// stored contiguously.  Returns their number (the same in every thread) and,
+// in *below, the largest key under `thr`.  Nothing is written when they do not
+// fit the region (more than a.R).  The entries are read by k_finish, a later
+// kernel.  `lds` holds kStageCap uint2 and is free on return.
 template <int DT, bool ZKEYS>
-__device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int start, int end, const u32 (&kz)[kEPT],
-                                           u32 thr, float T, Scratch& sc, u32* below_out) {
+__device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int start, const u32 (&kz)[kEPT], u32 thr,
+                                           float T, unsigned char* lds, Scratch& sc, u32* below_out) {
   constexpr int VW = (DT == QS_DTYPE_F32) ? 4 : 8;
   constexpr int NV = kEPT / VW;
   constexpr int NW = (NV + 1) / 2;  // counts per vector packed two to a word (16-bit fields)
@@ -1277,7 +1327,7 @@ __device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int 
       const u32 k = kz[v * VW + j];
       const bool in = k >= thr;
       pk[v >> 1] += (in ? 1u : 0u) << (16 * (v & 1));
-      below = (!in && k > below) ? k : below;
+      below = in ? below : (k > below ? k : below);
     }
   }
   u32 inc[NW];
@@ -1308,44 +1358,55 @@ __device__ __forceinline__ u32 emit_region(const Args& a, int row, int blk, int 
   for (int v = 0; v < NV; ++v) total += (tot[v >> 1] >> (16 * (v & 1))) & 0xffffu;
   *below_out = bmax;
   if (total > (u32)a.R) return total;
-  uint4* rg = a.cand + ((size_t)row * a.G + blk) * a.R;
+  // stage (chunk index, key) at the final positions
+  u32* stg_i = (u32*)lds;           // [kStageCap] chunk index
+  u32* stg_k = stg_i + kStageCap;   // [kStageCap] key
   u32 run = 0u;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int sh = 16 * (v & 1);
     u32 pos = run + (((base[v >> 1] + inc[v >> 1] - pk[v >> 1]) >> sh) & 0xffffu);
-    const u32 e0 = (u32)(start + (v * kThreads + tid) * VW);
+    const u32 l0 = (u32)((v * kThreads + tid) * VW);
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
       u32 k = kz[v * VW + j];
+      asm volatile("" : "+v"(k));  // compared again here: keeping 32 lane masks costs registers
       if (k >= thr) {
-        asm volatile("" : "+v"(k));  // the entry is computed here, for written tokens only
-        const float q = ZKEYS ? f_of_key(k) / T : f_of_key(k);
-        const double y = y_of(q);
-        const double fl = floor(y);
-        rg[pos] = make_uint4(e0 + (u32)j, skey(q), mant24(exp2_poly((float)(y - fl))), (u32)(int)fl);
+        stg_i[pos] = l0 + (u32)j;
+        stg_k[pos] = k;
         ++pos;
       }
     }
     run += (tot[v >> 1] >> sh) & 0xffffu;
   }
+  __syncthreads();
+  // the entries, one per thread
+  uint4* rg = a.cand + ((size_t)row * a.G + blk) * a.R;
+  for (u32 i = (u32)tid; i < total; i += kThreads) {
+    const uint2 s = make_uint2(stg_i[i], stg_k[i]);
+    const float q = ZKEYS ? f_of_key(s.y) / T : f_of_key(s.y);
+    const double y = y_of(q);
+    const double fl = floor(y);
+    rg[i] = make_uint4((u32)start + s.x, skey(q), mant24(exp2_poly((float)(y - fl))), (u32)(int)fl);
+  }
+  __syncthreads();
   return total;
 }
 
 // ---------------------------------------------------------------- finishing a row from its regions
 
-// finish_row with at most 256 merged candidates, in id order in LDS (ids,
-// keys, packed weights): one per thread.  Each candidate's rank in (q desc,
+// finish_row with at most 256 members, in id order in LDS (st: ids, keys,
+// packed weights, kThreads each): one per thread.  Each candidate's rank in (q desc,
 // id asc) order is counted directly, the candidates are placed in that order,
 // and one prefix sum in it gives the top-k set, its mass and the top-p
 // boundary; a second, in id order, gives the draw.
 template <bool TOPK>
 __device__ __forceinline__ bool finish_small(const Args& a, const RowParams& p, int row, u32 m, int N, u32 nout,
-                                             unsigned char* lds, Scratch& sc) {
+                                             u32* st, Scratch& sc) {
   const int tid = threadIdx.x;
-  u32* st_id = (u32*)lds;
-  u32* st_key = st_id + kFinCap;
-  u32* st_wp = st_key + kFinCap;
+  u32* st_id = st;
+  u32* st_key = st_id + kThreads;
+  u32* st_wp = st_key + kThreads;
   const bool have = (u32)tid < m;
   const u32 mkey = have ? st_key[tid] : 0u, mid = have ? st_id[tid] : 0u, mwp = have ? st_wp[tid] : 0u;
   // rank: members with a larger key, or the same key and a smaller id (an earlier slot)
@@ -1431,7 +1492,11 @@ __device__ __forceinline__ bool finish_small(const Args& a, const RowParams& p, 
 // a top-k row (TOPK: entries hold z keys; k-select, then a proof that no token
 // left out could be in the top-k set) or the first workgroup of a peaked mass
 // row (entries hold q keys; `kthr` drops those outside the row's window).
-// The regions are gathered in id order into registers (kFinPer per thread).
+// The regions are gathered in id order into registers: thread t holds the
+// concatenated entries [t * per, t * per + per), so register order is id
+// order.  At most 256 members go through finish_small; more are resolved over
+// one 2048-bin histogram of their keys (count and mass per bin), whose single
+// scan places the k-th key and the top-p boundary in their bins.
 // False if the candidates cannot be proven to hold the answer; the caller then
 // resolves the row with resolve_single.
 template <bool TOPK>
@@ -1441,27 +1506,30 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
   const Slot* sl = a.slots + (size_t)row * a.G;
   const uint4* cd = a.cand + (size_t)row * a.G * a.R;
   // (written by k_sample, an earlier kernel on this stream: plain loads see it)
-  // ---- the regions' headers: one region per thread (G <= 256)
   u32* hoff = (u32*)lds;  // [kMaxChunks + 1] start of each region's entries in the concatenation
-  u32 cnt = 0u, tau = 0u, below = 0u;
+  WideLds& WL = *(WideLds*)(lds + kHoffBytes);
+  SelLds* SL = (SelLds*)(lds + kHoffBytes + sizeof(WideLds));
+  // ---- the regions' headers: one region per thread (G <= 256)
+  u32 cnt = 0u, hx[3] = {0u, 0u, 0u};  // tau, overflow, below
   if (tid < a.G) {
     cnt = sl[tid].nb;
     if (TOPK) {
-      tau = sl[tid].tau;
-      below = sl[tid].below;
+      hx[0] = sl[tid].tau;
+      hx[2] = sl[tid].below;
     }
   }
-  u32 ovf = cnt == 0xffffffffu ? 1u : 0u;
-  if (ovf) cnt = 0u;
+  if (cnt == 0xffffffffu) {
+    hx[1] = 1u;
+    cnt = 0u;
+  }
   u32 m0;
-  const u32 coff = block_scan_u32(cnt, sc, &m0);
-  u32 tstar = tau;
-  block_max3(tstar, ovf, below, sc);  // its barriers also order hoff below
+  const u32 coff = block_scan_max<3>(cnt, hx, sc, &m0);
+  const u32 tstar = hx[0], below = hx[2];
   if (tid < a.G) hoff[tid] = coff;
   if (tid == 0) hoff[a.G] = m0;
   __syncthreads();
   QS_TR(11);
-  if (ovf) return give_up(a, row, kWhyRegion);
+  if (hx[1]) return give_up(a, row, kWhyRegion);
   if (m0 > (u32)(kThreads * kGatherPer)) return give_up(a, row, kWhyMerge);
   // ---- this thread's share of the concatenated entries (id order): flat
   // indices [f0, f0 + per); all loads issued before any is used
@@ -1486,101 +1554,95 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
       ent[q] = cd[(size_t)g * a.R + (f - hoff[g])];
     }
   }
-  // ---- entries at or above the threshold, compacted in id order through LDS;
-  // the weights need the row scale N = the largest octave among them
+  // the histogram is cleared while the loads are in flight (the exchange
+  // below orders it before its use)
+  for (int i = tid; i < kWide; i += kThreads) {
+    WL.cnt[i] = 0u;
+    WL.mlo[i] = 0ull;
+    WL.mhi[i] = 0ull;
+  }
+  if (tid == 0) {
+    sc.i[1] = -1;  // wide_find result slots
+    sc.i[2] = -1;
+    sc.u[0] = sc.u[1] = sc.u[2] = sc.u[3] = 0u;  // key range of the k-th's and the boundary's bins
+  }
+  // ---- members: entries at or above the threshold.  One exchange gives
+  // their number and positions, the row scale N (their largest octave), the
+  // largest q key of the tokens left out, and their key range.
   const u32 thr = TOPK ? skey(f_of_key(tstar) / p.T) : kthr;
-  u32 flags = 0u, npass = 0u, dropmax = 0u;
+  u32 memb = 0u, npass = 0u, dropmax = 0u, kmx = 0u, nkmn = 0u;
   int nmax = (int)0x80000000u;
 #pragma unroll
   for (int q = 0; q < kGatherPer; ++q) {
     if ((u32)q < per && f0 + (u32)q < m0) {
       const u32 k = ent[q].y;
       if (k >= thr) {
-        flags |= 1u << q;
+        memb |= 1u << q;
         ++npass;
         nmax = (int)ent[q].w > nmax ? (int)ent[q].w : nmax;
+        kmx = k > kmx ? k : kmx;
+        nkmn = ~k > nkmn ? ~k : nkmn;
       } else {
         dropmax = k > dropmax ? k : dropmax;
       }
     }
   }
-  u32 m;
-  const u32 off = block_scan_u32(npass, sc, &m);
-  u32 nout = 0u, nmx = (u32)nmax ^ 0x80000000u, dummy = 0u;
+  QS_TR(1);
+  u32 sx[4] = {dropmax, (u32)nmax ^ 0x80000000u, kmx, nkmn};
   if (TOPK) {
     // largest q key of the tokens left out: dropped entries, and below each region's threshold
     const u32 bq = below ? skey(f_of_key(below) / p.T) : 0u;
-    nout = dropmax > bq ? dropmax : bq;
+    sx[0] = dropmax > bq ? dropmax : bq;
   }
-  block_max3(nout, nmx, dummy, sc);
-  const int N = (int)(nmx ^ 0x80000000u);
-  if (m > (u32)kFinCap) return give_up(a, row, kWhyMerge);
+  u32 m;
+  const u32 off = block_scan_max<4>(npass, sx, sc, &m);
+#ifdef QS_TRACE
+  if (a.trace && tid == 0) {
+    ((u32*)(a.ctl + row))[40] = m0;
+    ((u32*)(a.ctl + row))[41] = m;
+  }
+#endif
+  const u32 nout = TOPK ? sx[0] : 0u;
+  const int N = (int)(sx[1] ^ 0x80000000u);
   if (TOPK && m < (u32)p.k) return give_up(a, row, kWhyFewer);
-  u32* st_id = (u32*)lds;
-  u32* st_key = st_id + kFinCap;
-  u32* st_wp = st_key + kFinCap;
-  {
+  u32 key[kGatherPer], id[kGatherPer], wp[kGatherPer];
+#pragma unroll
+  for (int q = 0; q < kGatherPer; ++q) {
+    const int r = (int)ent[q].w - N + kWindow;
+    key[q] = ent[q].y;
+    id[q] = ent[q].x;
+    wp[q] = (((memb >> q) & 1u) && r >= 0) ? ((u32)r << 24) | ent[q].z : 0u;
+  }
+  if (m <= (u32)kThreads) {
+    // few members: one per thread, in id order, through LDS
+    u32* st = (u32*)(lds + kHoffBytes);  // [3][kThreads] ids, keys, packed weights
     u32 pos = off;
 #pragma unroll
     for (int q = 0; q < kGatherPer; ++q) {
-      if ((flags >> q) & 1u) {
-        const int r = (int)ent[q].w - N + kWindow;
-        st_id[pos] = ent[q].x;
-        st_key[pos] = ent[q].y;
-        st_wp[pos] = r >= 0 ? ((u32)r << 24) | ent[q].z : 0u;
+      if ((memb >> q) & 1u) {
+        st[pos] = id[q];
+        st[kThreads + pos] = key[q];
+        st[2 * kThreads + pos] = wp[q];
         ++pos;
       }
     }
+    __syncthreads();
+    QS_TR(2);
+    return finish_small<TOPK>(a, p, row, m, N, nout, st, sc);
   }
-  __syncthreads();
-  if (m <= (u32)kThreads) return finish_small<TOPK>(a, p, row, m, N, nout, lds, sc);
-  u32 key[kFinPer], id[kFinPer], wp[kFinPer], memb = 0u;
-  u32 kmx = 0u;
-#pragma unroll
-  for (int j = 0; j < kFinPer; ++j) {
-    const u32 i = (u32)(tid * kFinPer + j);
-    if (i < m) {
-      key[j] = st_key[i];
-      id[j] = st_id[i];
-      wp[j] = st_wp[i];
-      memb |= 1u << j;
-      kmx = key[j] > kmx ? key[j] : kmx;
-    } else {
-      key[j] = 0u;
-      id[j] = 0u;
-      wp[j] = 0u;
-    }
-  }
-  __syncthreads();  // the staging area becomes the histogram and select buffers
-  QS_TR(5);
-  // ---- one histogram of the members over 11 bits of the key (count and mass
-  // per bin), scanned once from the top; the bins holding the k-th key and the
-  // top-p boundary are then resolved among their own members only
-  WideLds& WL = *(WideLds*)lds;
-  SelLds* SL = (SelLds*)(lds + sizeof(WideLds));
-  u32 nkmn = 0u, anym = memb ? 1u : 0u, kmx2 = kmx;
-#pragma unroll
-  for (int j = 0; j < kFinPer; ++j)
-    if ((memb >> j) & 1u) nkmn = ~key[j] > nkmn ? ~key[j] : nkmn;
-  block_max3(nkmn, anym, kmx2, sc);
-  if (!anym) return give_up(a, row, kWhyKSelect);
-  const u32 kfirst = uni(~nkmn), kdiff = uni(kmx2) ^ kfirst;
+  // ---- the histogram: bits [lob, lob + 11) of the key.  Bits above hib are
+  // common to all members, so the digit is monotone in the key; with lob == 0
+  // a bin holds a single key, (kfirst & ~(kWide - 1)) | bin.
+  const u32 kfirst = ~sx[3], kdiff = sx[2] ^ kfirst;
   const int hib = kdiff ? 31 - __clz(kdiff) : 0;
   const int lob = hib >= kWideBits - 1 ? hib - (kWideBits - 1) : 0;
-  // bits above hib are common to all members, so the digit is monotone in the key;
-  // with lob == 0 a bin holds a single key, (kfirst & ~(kWide - 1)) | bin
-  for (int i = tid; i < kWide; i += kThreads) {
-    WL.cnt[i] = 0u;
-    WL.mlo[i] = 0ull;
-    WL.mhi[i] = 0ull;
-  }
-  __syncthreads();
+  auto digit = [&](u32 k) { return (int)((k >> lob) & (u32)(kWide - 1)); };
 #pragma unroll
-  for (int j = 0; j < kFinPer; ++j) {
-    if ((memb >> j) & 1u) {
-      const u32 d = (key[j] >> lob) & (u32)(kWide - 1);
+  for (int q = 0; q < kGatherPer; ++q) {
+    if ((memb >> q) & 1u) {
+      const int d = digit(key[q]);
       atomicAdd(&WL.cnt[d], 1u);
-      u32 wj = wp[j];
+      u32 wj = wp[q];
       asm volatile("" : "+v"(wj));
       const u64 w = wunpack(wj);
       if (w) {
@@ -1590,35 +1652,52 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
     }
   }
   __syncthreads();
-  Acc wmine = {0, 0, 0};
+  QS_TR(4);
+  Acc wbin[kWidePer], wmine = {0, 0, 0};
 #pragma unroll
-  for (int i = 0; i < kWidePer; ++i) wmine = acc_add(wmine, wide_bin(WL, kWide - 1 - (tid * kWidePer + i)));
+  for (int i = 0; i < kWidePer; ++i) {
+    wbin[i] = wide_bin(WL, kWide - 1 - (tid * kWidePer + i));
+    wmine = acc_add(wmine, wbin[i]);
+  }
   Acc wtot;
   const Acc wex = block_scan_acc(wmine, sc, &wtot);
-  auto digit = [&](u32 k) { return (int)((k >> lob) & (u32)(kWide - 1)); };
+  QS_TR(8);
+  // the key range of bin b's members (r0, r1 in sc.u) is a single key iff it
+  // collapses: one LDS max per member of the bin, one barrier
+  auto bin_single = [&](int b, int r0, u32* kv) {
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q) {
+      if (((memb >> q) & 1u) && digit(key[q]) == b) {
+        atomicMax(&sc.u[r0], key[q]);
+        atomicMax(&sc.u[r0 + 1], ~key[q]);
+      }
+    }
+    __syncthreads();
+    const u32 hi = sc.u[r0], nlo = sc.u[r0 + 1];
+    *kv = hi;
+    return hi == ~nlo;
+  };
   // ---- top-k: the k-th largest q, and the proof that the candidates hold the top-k set
   u32 kappa = 0u;
   int bk = -1;
   Acc kb = {0, 0, 0}, ka = {0, 0, 0};  // bins above kappa's, kappa's bin
+  bool ksingle = true;                 // kappa's bin holds kappa only
+  u128 S;
   if (TOPK) {
-    wide_find(WL, wex, wmine, false, (u128)(p.k - 1), sc, &bk, &kb, &ka);
+    wide_find(wbin, wex, false, (u128)(p.k - 1), sc, 0, &bk, &kb, &ka);
+    QS_TR(10);
     if (bk < 0) return give_up(a, row, kWhyKSelect);
     if (lob == 0) {
       kappa = (kfirst & ~(u32)(kWide - 1)) | (u32)bk;
+    } else if (bin_single(bk, 0, &kappa)) {
+      // kappa: the bin's single key
     } else {
-      u32 mk = 0u, bmx = 0u, bnmn = 0u, dummy = 0u;
+      u32 mk = 0u;
 #pragma unroll
-      for (int j = 0; j < kFinPer; ++j) {
-        if (((memb >> j) & 1u) && digit(key[j]) == bk) {
-          mk |= 1u << j;
-          bmx = key[j] > bmx ? key[j] : bmx;
-          bnmn = ~key[j] > bnmn ? ~key[j] : bnmn;
-        }
-      }
-      block_max3(bmx, bnmn, dummy, sc);
-      if (bmx == ~bnmn) {
-        kappa = bmx;  // the bin holds a single key
-      } else {
+      for (int q = 0; q < kGatherPer; ++q)
+        if (((memb >> q) & 1u) && digit(key[q]) == bk) mk |= 1u << q;
+      {
+        ksingle = false;
         const SelOut sk = reg_select<false>(key, mk, wp, (u128)(p.k - 1 - kb.c), SL, sc);
         if (!sk.ok) return give_up(a, row, kWhyKSelect);
         kappa = sk.val;
@@ -1627,14 +1706,15 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
     QS_TR(6);
     // every token left out has a q key <= nout: it must be below the k-th
     if (nout > 0u && nout >= kappa) return give_up(a, row, kWhyIncomplete);
-  }
-  u128 S;
-  if (TOPK) {
-    u128 sv = 0;
+    if (ksingle) {
+      S = acc_mass(kb) + acc_mass(ka);
+    } else {
+      u128 sv = 0;
 #pragma unroll
-    for (int j = 0; j < kFinPer; ++j)
-      if (((memb >> j) & 1u) && key[j] >= kappa) sv += (u128)wunpack(wp[j]);
-    S = uni128(block_sum128(sv, sc));
+      for (int q = 0; q < kGatherPer; ++q)
+        if (((memb >> q) & 1u) && key[q] >= kappa) sv += (u128)wunpack(wp[q]);
+      S = uni128(block_sum128(sv, sc));
+    }
   } else {
     S = acc_mass(wtot);
   }
@@ -1644,46 +1724,52 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
   if (p.topp_on) {
     // the first token (q desc, id asc) whose inclusive mass exceeds floor(top_p * S)
     const u128 Tp = uni128(mul_frac(S, p.tp));
-    int bp;
-    Acc pb, pa;
-    bool restrict_k = false;  // the boundary lies in kappa's bin, among its keys >= kappa
-    if (TOPK && Tp >= acc_mass(kb)) {
-      bp = bk;
-      pb = kb;
-      pa = ka;
-      restrict_k = true;
-    } else {
-      wide_find(WL, wex, wmine, true, Tp, sc, &bp, &pb, &pa);
-      if (bp < 0) return give_up(a, row, kWhyTopP);
-    }
     u128 A;
     Acc at;
-    if (lob == 0) {
-      kp = (kfirst & ~(u32)(kWide - 1)) | (u32)bp;
-      A = acc_mass(pb);
-      at = pa;
-    } else {
-      u32 mp = 0u, bmx = 0u, bnmn = 0u, dummy = 0u;
+    if (TOPK && Tp >= acc_mass(kb)) {
+      // the boundary lies in kappa's bin, among its keys >= kappa
+      if (ksingle) {
+        kp = kappa;
+        A = acc_mass(kb);
+        at = ka;
+      } else {
+        u32 mp = 0u;
 #pragma unroll
-      for (int j = 0; j < kFinPer; ++j) {
-        if (((memb >> j) & 1u) && digit(key[j]) == bp && (!restrict_k || key[j] >= kappa)) {
-          mp |= 1u << j;
-          bmx = key[j] > bmx ? key[j] : bmx;
-          bnmn = ~key[j] > bnmn ? ~key[j] : bnmn;
-        }
+        for (int q = 0; q < kGatherPer; ++q)
+          if (((memb >> q) & 1u) && digit(key[q]) == bk && key[q] >= kappa) mp |= 1u << q;
+        const SelOut sp = reg_select<true>(key, mp, wp, Tp - acc_mass(kb), SL, sc);
+        if (!sp.ok) return give_up(a, row, kWhyTopP);
+        kp = sp.val;
+        A = acc_mass(kb) + acc_mass(sp.before);
+        at = sp.at;
       }
-      block_max3(bmx, bnmn, dummy, sc);
-      if (!restrict_k && bmx == ~bnmn) {
-        // the bin holds a single key
-        kp = bmx;
+    } else {
+      int bp;
+      Acc pb, pa;
+      wide_find(wbin, wex, true, Tp, sc, 1, &bp, &pb, &pa);
+      QS_TR(12);
+      if (bp < 0) return give_up(a, row, kWhyTopP);
+      u32 bkey = 0u;
+      if (lob == 0) {
+        kp = (kfirst & ~(u32)(kWide - 1)) | (u32)bp;
+        A = acc_mass(pb);
+        at = pa;
+      } else if (bin_single(bp, 2, &bkey)) {
+        kp = bkey;
         A = acc_mass(pb);
         at = pa;
       } else {
-        const SelOut sp = reg_select<true>(key, mp, wp, Tp - acc_mass(pb), SL, sc);
-        if (!sp.ok) return give_up(a, row, kWhyTopP);
-        kp = sp.val;
-        A = acc_mass(pb) + acc_mass(sp.before);
-        at = sp.at;
+        u32 mp = 0u;
+#pragma unroll
+        for (int q = 0; q < kGatherPer; ++q)
+          if (((memb >> q) & 1u) && digit(key[q]) == bp) mp |= 1u << q;
+        {
+          const SelOut sp = reg_select<true>(key, mp, wp, Tp - acc_mass(pb), SL, sc);
+          if (!sp.ok) return give_up(a, row, kWhyTopP);
+          kp = sp.val;
+          A = acc_mass(pb) + acc_mass(sp.before);
+          at = sp.at;
+        }
       }
     }
     QS_TR(14);
@@ -1696,16 +1782,16 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
       // the boundary member: tie member jb in id order, which is register order
       u32 c = 0u;
 #pragma unroll
-      for (int j = 0; j < kFinPer; ++j) c += (((memb >> j) & 1u) && key[j] == kp) ? 1u : 0u;
+      for (int q = 0; q < kGatherPer; ++q) c += (((memb >> q) & 1u) && key[q] == kp) ? 1u : 0u;
       if (tid == 0) sc.r[5] = 0xffffffffu;
       u32 ct;
       const u32 ex = block_scan_u32(c, sc, &ct);
       if (jb >= ex && jb < (u64)ex + c) {
         u32 r = ex;
 #pragma unroll
-        for (int j = 0; j < kFinPer; ++j) {
-          if (((memb >> j) & 1u) && key[j] == kp) {
-            if (r == (u32)jb) sc.r[5] = id[j];
+        for (int q = 0; q < kGatherPer; ++q) {
+          if (((memb >> q) & 1u) && key[q] == kp) {
+            if (r == (u32)jb) sc.r[5] = id[q];
             ++r;
           }
         }
@@ -1722,10 +1808,10 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
   u32 keptm = 0u;
   u128 mine = 0;
 #pragma unroll
-  for (int j = 0; j < kFinPer; ++j) {
-    if (((memb >> j) & 1u) && (key[j] > kp || (key[j] == kp && id[j] <= idp))) {
-      keptm |= 1u << j;
-      mine += (u128)wunpack(wp[j]);
+  for (int q = 0; q < kGatherPer; ++q) {
+    if (((memb >> q) & 1u) && (key[q] > kp || (key[q] == kp && id[q] <= idp))) {
+      keptm |= 1u << q;
+      mine += (u128)wunpack(wp[q]);
     }
   }
   if (tid == 0) sc.r[6] = 0xffffffffu;
@@ -1737,11 +1823,11 @@ __device__ __forceinline__ bool finish_row(const Args& a, const RowParams& p, in
       u128 run = lo;
       bool found = false;
 #pragma unroll
-      for (int j = 0; j < kFinPer; ++j) {
-        if (!found && ((keptm >> j) & 1u)) {
-          run += (u128)wunpack(wp[j]);
+      for (int q = 0; q < kGatherPer; ++q) {
+        if (!found && ((keptm >> q) & 1u)) {
+          run += (u128)wunpack(wp[q]);
           if (run > t) {
-            sc.r[6] = id[j];
+            sc.r[6] = id[q];
             found = true;
           }
         }
@@ -1791,140 +1877,125 @@ __device__ __forceinline__ void bracket_bins(const u64* g, u64 err, u128 Tp, int
   *bhi = hi;
 }
 
-// The histogram bin of y in a flat mass row.
-__device__ __forceinline__ int mass_bin(double y, double ylo, double bscale) {
-  const int b = (int)((y - ylo) * bscale);
-  return b < 0 ? 0 : (b > kBins - 1 ? kBins - 1 : b);
+// Histogram bins of a flat mass row, linear in q from q0 with scale s:
+// bin(q) = (int)clamp((q - q0) * s, 0, kBins - 1) in fp32, non-decreasing in q
+// and so in the key.
+struct QBins {
+  float q0, s;
+  __device__ __forceinline__ int bin(float q) const {
+    const float x = fminf(fmaxf((q - q0) * s, 0.0f), (float)(kBins - 1));
+    return (int)x;
+  }
+  // The smallest key in [1, key(+inf)] whose bin is at least b (b <= kBins - 1).
+  __device__ __forceinline__ u32 first_key(int b) const {
+    u32 lo = 1u, hi = 0xff800000u;
+    while (lo < hi) {
+      const u32 mid = lo + ((hi - lo) >> 1);
+      if (bin(f_of_key(mid)) >= b) hi = mid; else lo = mid + 1u;
+    }
+    return lo;
+  }
+};
+__device__ __forceinline__ QBins qbins_of(float qlo, float qhi) {
+  QBins r;
+  r.q0 = qlo;
+  r.s = qhi > qlo ? (float)kBins / (qhi - qlo) : 0.0f;
+  return r;
 }
 
-// Locates the drawn token inside chunk g: kept tokens (key > kp || (key == kp
-// && id <= idp)) in id order, the first whose inclusive mass within the chunk
-// exceeds tl.  Re-reads the chunk; thread t takes the kEPT tokens from
-// start + t * kEPT.  Returns the id (0xffffffff if none).
+// Per segment (vector v, this wave) of a k_sample workgroup: the exact sum of
+// the lanes' lo + hi * 2^64, written to sgm[2 * (v * kWaves + wave)].
+template <int NV>
+__device__ __forceinline__ void store_segments(u64* sgm, const u64 (&lo)[NV], const u32 (&hi)[NV]) {
+  const int wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const u128 m = wave_sum128(lo[v], hi[v]);
+    if (lane_id() == 0) {
+      sgm[2 * (v * kWaves + wv)] = (u64)m;
+      sgm[2 * (v * kWaves + wv) + 1] = (u64)(m >> 64);
+    }
+  }
+}
+
+// Segment s of chunk g, s = v * kWaves + w: the tokens that wave w of the
+// chunk's k_sample workgroup held in vector v, the ids
+// [seg_first(g, s), seg_first(g, s) + 64 * VW) (clipped at the row's end).
 template <int DT>
-__device__ __forceinline__ u32 draw_in_chunk(const Args& a, const RowParams& p, int row, int g, int N, u32 kp, u32 idp,
-                                             u128 tl, unsigned char* lds, Scratch& sc) {
+__device__ __forceinline__ int seg_first(int g, int s) {
+  constexpr int VW = ChunkLoad<DT>::VW;
+  return g * kCH + ((s / kWaves) * kThreads + (s % kWaves) * 64) * VW;
+}
+
+// Re-reads segment s of chunk g (one or two tokens per thread, in id order).
+// DRAW: the id of the first kept token (key > kp || (key == kp && id <= idp))
+// whose inclusive mass within the segment exceeds tl.  Otherwise: the id of
+// the token of rank `rank` (0-based, id order) among those whose key is kp.
+// 0xffffffff if there is none.  `plds` holds the chunk's penalty table.
+template <int DT, bool DRAW>
+__device__ __forceinline__ u32 seg_locate(const Args& a, const RowParams& p, int row, int g, int s, int N, u32 kp,
+                                          u32 idp, u128 tl, u32 rank, unsigned char* plds, Scratch& sc) {
+  constexpr int VW = ChunkLoad<DT>::VW;
+  constexpr int E = 64 * VW / kThreads;  // tokens per thread
   const int tid = threadIdx.x;
   const int start = g * kCH, end = min(a.V, start + kCH);
   PenTable pt;
-  pt.bits = (u32*)lds;
+  pt.bits = (u32*)plds;
   pt.wpre = pt.bits + (kCH >> 5);
   pt.cnts = pt.wpre + (kCH >> 5);
-  const int e0 = start + tid * kEPT;
-  float z[kEPT];
-  {
-    constexpr int ESZ = (DT == QS_DTYPE_F32) ? 4 : 2;
-    constexpr int VW = 16 / ESZ;
-    const char* rp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * ESZ;
-    const bool vec = ((((uintptr_t)a.logits) | ((size_t)a.row_stride * ESZ)) & 15) == 0;
-#pragma unroll
-    for (int v = 0; v < kEPT / VW; ++v) {
-      const int ev = e0 + v * VW;
-      if (vec && ev + VW <= end) {
-        const uint4 r = *(const uint4*)(rp + (size_t)ev * ESZ);
-        const u32 w4[4] = {r.x, r.y, r.z, r.w};
-        if (DT == QS_DTYPE_F32) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) z[v * 4 + j] = __uint_as_float(w4[j]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            z[v * 8 + 2 * j] = bf16_to_f32(w4[j] & 0xffffu);
-            z[v * 8 + 2 * j + 1] = bf16_to_f32(w4[j] >> 16);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < VW; ++j) z[v * VW + j] = (ev + j < end) ? load_logit<DT>(a, row, ev + j) : 0.0f;
-      }
-    }
-  }
   if (p.pen_on) pen_build(a, row, start, end, pt, sc);
-  u128 mine = 0;
+  const int e0 = seg_first<DT>(g, s) + tid * E;
+  float q[E];
+  u32 k[E];
 #pragma unroll
-  for (int j = 0; j < kEPT; ++j) {
+  for (int j = 0; j < E; ++j) {
     const int e = e0 + j;
-    if (e < end) {
-      float zz = z[j];
-      if (p.pen_on) {
-        const u32 cnt = pen_count(pt, e - start);
-        if (cnt) zz = apply_penalty(zz, cnt, p.rep, p.pres, p.freq);
-      }
-      const float q = zz / p.T;
-      z[j] = q;
-      const u32 k = skey(q);
-      if (k > kp || (k == kp && (u32)e <= idp)) mine += (u128)weight_of(q, N);
+    float zz = e < end ? load_logit<DT>(a, row, e) : 0.0f;
+    if (p.pen_on && e < end) {
+      const u32 cn = pen_count(pt, e - start);
+      if (cn) zz = apply_penalty(zz, cn, p.rep, p.pres, p.freq);
     }
+    q[j] = zz / p.T;
+    k[j] = e < end ? skey(q[j]) : 0u;
   }
   if (tid == 0) sc.r[9] = 0xffffffffu;
-  Acc tot;
-  const Acc ex = block_scan_acc(acc_of(mine, 0u), sc, &tot);
-  {
-    const u128 lo = acc_mass(ex);
-    if (tl >= lo && tl < lo + mine) {
-      u128 run = lo;
+  if (DRAW) {
+    u64 w[E];
+    u128 mine = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const bool kept = k[j] && (k[j] > kp || (k[j] == kp && (u32)(e0 + j) <= idp));
+      w[j] = kept ? weight_of(q[j], N) : 0ull;
+      mine += (u128)w[j];
+    }
+    Acc tot;
+    const Acc ex = block_scan_acc(acc_of(mine, 0u), sc, &tot);
+    u128 run = acc_mass(ex);
+    if (tl >= run && tl < run + mine) {
       bool found = false;
 #pragma unroll
-      for (int j = 0; j < kEPT; ++j) {
-        const int e = e0 + j;
-        if (!found && e < end) {
-          const u32 k = skey(z[j]);
-          if (k > kp || (k == kp && (u32)e <= idp)) {
-            run += (u128)weight_of(z[j], N);
-            if (run > tl) {
-              sc.r[9] = (u32)e;
-              found = true;
-            }
-          }
+      for (int j = 0; j < E; ++j) {
+        run += (u128)w[j];
+        if (!found && run > tl) {
+          sc.r[9] = (u32)(e0 + j);
+          found = true;
         }
       }
     }
-  }
-  __syncthreads();
-  const u32 id = sc.r[9];
-  __syncthreads();
-  return id;
-}
-
-// The id of the member of rank `rank` (0-based, id order) among the tokens of
-// chunk g whose key is kp.  Re-reads the chunk like draw_in_chunk.
-template <int DT>
-__device__ __forceinline__ u32 rank_in_chunk(const Args& a, const RowParams& p, int row, int g, u32 kp, u32 rank,
-                                             unsigned char* lds, Scratch& sc) {
-  const int tid = threadIdx.x;
-  const int start = g * kCH, end = min(a.V, start + kCH);
-  PenTable pt;
-  pt.bits = (u32*)lds;
-  pt.wpre = pt.bits + (kCH >> 5);
-  pt.cnts = pt.wpre + (kCH >> 5);
-  if (p.pen_on) pen_build(a, row, start, end, pt, sc);
-  const int e0 = start + tid * kEPT;
-  u32 mk = 0u, c = 0u;  // bit j: token e0 + j has key kp
+  } else {
+    u32 c = 0u;
 #pragma unroll
-  for (int j = 0; j < kEPT; ++j) {
-    const int e = e0 + j;
-    if (e < end) {
-      float zz = load_logit<DT>(a, row, e);
-      if (p.pen_on) {
-        const u32 cnt = pen_count(pt, e - start);
-        if (cnt) zz = apply_penalty(zz, cnt, p.rep, p.pres, p.freq);
-      }
-      if (skey(zz / p.T) == kp) {
-        mk |= 1u << j;
-        ++c;
-      }
-    }
-  }
-  if (tid == 0) sc.r[9] = 0xffffffffu;
-  u32 ct;
-  const u32 ex = block_scan_u32(c, sc, &ct);
-  if (rank >= ex && rank < ex + c) {
-    u32 r = ex;
+    for (int j = 0; j < E; ++j) c += (k[j] && k[j] == kp) ? 1u : 0u;
+    u32 ct;
+    const u32 ex = block_scan_u32(c, sc, &ct);
+    if (rank >= ex && rank < ex + c) {
+      u32 r = ex;
 #pragma unroll
-    for (int j = 0; j < kEPT; ++j) {
-      if ((mk >> j) & 1u) {
-        if (r == rank) sc.r[9] = (u32)(e0 + j);
-        ++r;
+      for (int j = 0; j < E; ++j) {
+        if (k[j] && k[j] == kp) {
+          if (r == rank) sc.r[9] = (u32)(e0 + j);
+          ++r;
+        }
       }
     }
   }
@@ -1935,25 +2006,34 @@ __device__ __forceinline__ u32 rank_in_chunk(const Args& a, const RowParams& p, 
 }
 
 // LDS of the flat-row resolver: two select buffers; per chunk, the kept mass
-// of its bracket entries above the boundary key and its count of tokens at it.
+// of its bracket entries above the boundary key and its count of tokens at
+// it; per segment of the owner chunk, the same, and per segment of the chunk
+// holding the boundary token, its count of tokens at the boundary key.
 struct FlatLds {
   SelLds sel[2];
   u64 clo[kMaxChunks];
   u64 chi[kMaxChunks];
   u32 ckp[kMaxChunks];
+  u64 slo[kSegs];
+  u64 shi[kSegs];
+  u32 skp[kSegs];
+  u32 bkp[kSegs];
 };
 
 // A flat mass row after k_sample: the top-p boundary from the bracket entries
-// (topp) or none, the kept mass per chunk, the chunk holding the draw target,
-// and the token inside it.  With `topp` false every token is kept and the
-// chunk masses are the slots' s values.
+// (topp) or none; the kept mass per chunk and the chunk holding the draw
+// target; within it, the kept mass per segment and the segment holding the
+// target; the token inside that segment.  With `topp` false every token is
+// kept and the masses are the chunks' and segments' totals.
 template <int DT>
 __device__ __forceinline__ bool resolve_flat(const Args& a, const RowParams& p, int row, int N, bool topp, u128 Tp,
                                              bool bottom, unsigned char* lds, Scratch& sc) {
+  constexpr int NSEG = ChunkLoad<DT>::NV * kWaves;
   const int tid = threadIdx.x;
   const Slot* sl = a.slots + (size_t)row * a.G;
   RowCtl* c = a.ctl + row;
   FlatLds& F = *(FlatLds*)lds;
+  unsigned char* plds = lds + sizeof(FlatLds);
   // per-chunk mass above the bracket (topp) or of the whole chunk
   u128 ag = 0;
   if (tid < a.G) ag = topp ? mk128(ldc(&sl[tid].a_lo), ldc(&sl[tid].a_hi)) : mk128(ldc(&sl[tid].s_lo), ldc(&sl[tid].s_hi));
@@ -1966,20 +2046,27 @@ __device__ __forceinline__ bool resolve_flat(const Args& a, const RowParams& p, 
     F.chi[tid] = 0ull;
     F.ckp[tid] = 0u;
   }
+  if (tid < kSegs) {
+    F.slo[tid] = 0ull;
+    F.shi[tid] = 0ull;
+    F.skp[tid] = 0u;
+    F.bkp[tid] = 0u;
+  }
+  // bracket entries: key, count, chunk
+  u32 key[kFinPer], cnt[kFinPer], wp[kFinPer], cs[kFinPer], memb = 0u;
   if (topp) {
     const u32 m = ldc(&c->list_n);
     const u32 st = ldc(&c->status);
     const u64* lst = a.list + (size_t)row * kListCap;
-    u32 key[kFinPer], cnt[kFinPer], wp[kFinPer], memb = 0u;
-    int ch[kFinPer];
+    const u32 P = (min(m, (u32)kListCap) + kThreads - 1) / kThreads;  // entries per thread, <= kFinPer
 #pragma unroll
     for (int j = 0; j < kFinPer; ++j) {
-      const u32 i = (u32)(tid * kFinPer + j);
-      const bool in = i < m && i < (u32)kListCap;
+      const u32 i = (u32)tid * P + (u32)j;
+      const bool in = (u32)j < P && i < m && i < (u32)kListCap;
       const u64 e = in ? ldc(&lst[i]) : 0ull;
       key[j] = (u32)(e >> 32);
       cnt[j] = (u32)e & 0xffffu;
-      ch[j] = (int)(((u32)e >> 16) & 0xffu);
+      cs[j] = ((u32)e >> 16) & 0xffu;
       if (in) memb |= 1u << j;
     }
     const u128 A = block_sum128(ag, sc);
@@ -2007,12 +2094,13 @@ __device__ __forceinline__ bool resolve_flat(const Args& a, const RowParams& p, 
 #pragma unroll
     for (int j = 0; j < kFinPer; ++j) {
       if ((memb >> j) & 1u) {
+        const u32 ch = cs[j];
         if (key[j] > kp) {
           const u64 w = wunpack(wp[j]);
-          atomicAdd(&F.clo[ch[j]], (w & 0xffffffffull) * cnt[j]);
-          atomicAdd(&F.chi[ch[j]], (w >> 32) * cnt[j]);
+          atomicAdd(&F.clo[ch], (w & 0xffffffffull) * cnt[j]);
+          atomicAdd(&F.chi[ch], (w >> 32) * cnt[j]);
         } else if (key[j] == kp) {
-          atomicAdd(&F.ckp[ch[j]], cnt[j]);
+          atomicAdd(&F.ckp[ch], cnt[j]);
         }
       }
     }
@@ -2047,19 +2135,89 @@ __device__ __forceinline__ bool resolve_flat(const Args& a, const RowParams& p, 
     sc.w[17] = (u64)(tl >> 64);
   }
   __syncthreads();
-  const u32 owner = sc.r[8];
+  const int owner = (int)sc.r[8];
   const u128 tl = mk128(sc.w[16], sc.w[17]);
-  const u32 gb = sc.r[14], rb = sc.r[15];
+  const int gb = (int)sc.r[14];
+  const u32 rb = sc.r[15];
   __syncthreads();
   QS_TR(3);
-  if (owner == 0xffffffffu) return give_up(a, row, kWhyOwner);
+  if (owner < 0 || owner >= a.G) return give_up(a, row, kWhyOwner);
+  if (split && (gb < 0 || gb >= a.G)) return give_up(a, row, kWhyTie);
+  // ---- segments: tokens at kp per segment of chunk gb (for the boundary
+  // token) and the kept bracket entries per segment of the owner chunk, from
+  // those chunks' own (key, segment) lists
+  if (topp) {
+    const u32 no = ldc(&sl[owner].nse);
+    const u32 nb2 = split ? ldc(&sl[gb].nse) : 0u;
+    if (no == 0xffffffffu || nb2 == 0xffffffffu) return give_up(a, row, kWhyList);
+    const u64* so = a.sent + ((size_t)row * a.G + owner) * kSegEnt;
+    const u64* sbp = a.sent + ((size_t)row * a.G + (split ? gb : 0)) * kSegEnt;
+    for (u32 i = tid; i < no; i += kThreads) {
+      const u64 e = so[i];
+      const u32 k = (u32)(e >> 32), sg = ((u32)e >> 16) & 31u, n = (u32)e & 0xffffu;
+      if (k > kp) {
+        const u64 w = wunpack(wpack(f_of_key(k), N));
+        atomicAdd(&F.slo[sg], (w & 0xffffffffull) * n);
+        atomicAdd(&F.shi[sg], (w >> 32) * n);
+      } else if (k == kp) {
+        atomicAdd(&F.skp[sg], n);
+      }
+    }
+    for (u32 i = tid; i < nb2; i += kThreads) {
+      const u64 e = sbp[i];
+      if ((u32)(e >> 32) == kp) atomicAdd(&F.bkp[((u32)e >> 16) & 31u], (u32)e & 0xffffu);
+    }
+  }
+  const u64* sgm = a.segm + ((size_t)row * a.G + owner) * (2 * kSegs);
+  u128 ms = 0;
+  if (tid < NSEG) ms = mk128(sgm[2 * tid], sgm[2 * tid + 1]);
+  __syncthreads();
+  int sb = -1;
+  u32 rbs = 0u;
   if (split) {
-    if (gb == 0xffffffffu) return give_up(a, row, kWhyTie);
-    idp = rank_in_chunk<DT>(a, p, row, (int)gb, kp, rb, lds, sc);
+    // the boundary token: rank rb among chunk gb's tokens at kp, by segment
+    const u32 bc = tid < NSEG ? F.bkp[tid] : 0u;
+    if (tid == 0) sc.r[13] = 0xffffffffu;
+    u32 bt;
+    const u32 bx = block_scan_u32(bc, sc, &bt);
+    if (tid < NSEG && rb >= bx && rb < bx + bc) {
+      sc.r[13] = (u32)tid;
+      sc.r[12] = rb - bx;
+    }
+    __syncthreads();
+    sb = (int)sc.r[13];
+    rbs = sc.r[12];
+    __syncthreads();
+    if (sb < 0 || sb >= NSEG) return give_up(a, row, kWhyTie);
+    idp = seg_locate<DT, false>(a, p, row, gb, sb, N, kp, 0u, 0, rbs, plds, sc);
     if (idp == 0xffffffffu) return give_up(a, row, kWhyTie);
   }
   QS_TR(8);
-  const u32 chosen = draw_in_chunk<DT>(a, p, row, (int)owner, N, kp, idp, tl, lds, sc);
+  // kept mass per segment of the owner chunk (one segment per thread)
+  u128 km = 0;
+  if (tid < NSEG) {
+    u32 ks = F.skp[tid];  // tokens at kp in the segment, kept in id order up to the boundary token
+    if (split) {
+      if (owner > gb || (owner == gb && tid > sb)) ks = 0u;
+      else if (owner == gb && tid == sb) ks = rbs + 1u;
+    }
+    km = ms + mk128(F.slo[tid], 0) + ((u128)F.shi[tid] << 32) + (u128)wk * ks;
+  }
+  if (tid == 0) sc.r[11] = 0xffffffffu;
+  Acc stot;
+  const Acc sx = block_scan_acc(acc_of(km, 0u), sc, &stot);
+  if (tid < NSEG && tl >= acc_mass(sx) && tl < acc_mass(sx) + km) {
+    sc.r[11] = (u32)tid;
+    const u128 t2 = tl - acc_mass(sx);
+    sc.w[16] = (u64)t2;
+    sc.w[17] = (u64)(t2 >> 64);
+  }
+  __syncthreads();
+  const int os = (int)sc.r[11];
+  const u128 tl2 = mk128(sc.w[16], sc.w[17]);
+  __syncthreads();
+  if (os < 0 || os >= NSEG) return give_up(a, row, kWhyOwner);
+  const u32 chosen = seg_locate<DT, true>(a, p, row, owner, os, N, kp, idp, tl2, 0u, plds, sc);
   QS_TR(10);
   if (tid == 0)
     publish_result(a, row, chosen == 0xffffffffu ? -1ll : (long long)chosen, N, W, kp, idp, false, 2u);
@@ -2181,44 +2339,49 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
 
     // ================================================================ top-k
     // tau: at least kc tokens of the chunk are >= tau, kc covering this chunk's
-    // expected share of the row's top-k with a wide margin.  Each wave sorts
-    // its 64 per-thread maxima (shuffles) and takes the ceil(kc/4)-th largest;
-    // the workgroup takes the smallest of the four.
+    // expected share of the row's top-k with a wide margin.  Each wave takes
+    // the ceil(kc/4)-th largest of its 64 per-thread maxima (a bit-by-bit
+    // search on ballot counts); the workgroup takes the smallest of the four.
     float z[kEPT];
     load_chunk_pen<DT>(a, p, row, start, end, z, lds, sc);
     QS_TR(1);
+    // z keys without the NaN and -0 cases of skey (3 operations): they only
+    // choose which tokens are written, and a NaN or -0 among them can only make
+    // the written set look incomplete to k_finish (whose entries carry exact
+    // keys of q), never wrong
     u32 kz[kEPT];
-    u32 tm = 0u;
 #pragma unroll
     for (int i = 0; i < kEPT; ++i) {
-      kz[i] = ((i % VW) < lim[i / VW]) ? skey(z[i]) : 0u;
-      tm = kz[i] > tm ? kz[i] : tm;
+      const u32 u = __float_as_uint(z[i]);
+      kz[i] = u ^ ((u32)((int)u >> 31) | 0x80000000u);
     }
+    if (end - start < kCH) {  // the row's last chunk: tokens past the end get key 0
+#pragma unroll
+      for (int i = 0; i < kEPT; ++i) kz[i] = ((i % VW) < lim[i / VW]) ? kz[i] : 0u;
+    }
+    u32 tm = 0u;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) tm = kz[i] > tm ? kz[i] : tm;
     const float mu = (float)p.k / (float)a.G;
     int kc = (int)ceilf(mu) + 4 * (int)ceilf(sqrtf(mu)) + 4;
     kc = min(kc, min(p.k, kThreads));
-    const int kw = (kc + kWaves - 1) / kWaves;
-    const int lane = tid & 63;
-    u32 x = tm;
-    for (int k2 = 2; k2 <= 64; k2 <<= 1) {
-      for (int j = k2 >> 1; j > 0; j >>= 1) {
-        const u32 o = __shfl_xor(x, j, 64);
-        const bool take_small = ((lane & j) == 0) == ((lane & k2) != 0);
-        x = take_small ? (o < x ? o : x) : (o > x ? o : x);
-      }
+    const u32 kw = (u32)((kc + kWaves - 1) / kWaves);
+    u32 tw = 0u;  // the largest value with at least kw thread maxima at or above it
+    for (int b = 31; b >= 0; --b) {
+      const u32 cand = tw | (1u << b);
+      if ((u32)__popcll(__ballot(tm >= cand)) >= kw) tw = cand;
     }
-    const u32 tw = __shfl(x, kw - 1, 64);
-    if (lane == 0) sc.v[tid >> 6][6] = tw;
+    if (lane_id() == 0) sc.v[tid >> 6][6] = tw;
     __syncthreads();
     QS_TR(2);
     u32 tau = sc.v[0][6];
     for (int w = 1; w < kWaves; ++w) tau = sc.v[w][6] < tau ? sc.v[w][6] : tau;
     u32 below;
-    u32 total = emit_region<DT, true>(a, row, blk, start, end, kz, tau, p.T, sc, &below);
+    u32 total = emit_region<DT, true>(a, row, blk, start, kz, tau, p.T, lds, sc, &below);
     if (total > (u32)a.R) {
       // too many tokens at the threshold (ties): leave those at tau out
       if (tau != 0xffffffffu) ++tau;
-      total = emit_region<DT, true>(a, row, blk, start, end, kz, tau, p.T, sc, &below);
+      total = emit_region<DT, true>(a, row, blk, start, kz, tau, p.T, lds, sc, &below);
     }
     if (tid == 0) {
       Slot* sl = a.slots + (size_t)row * a.G + blk;
@@ -2249,7 +2412,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
     block_max3(kmx, nkmn, dummy, sc);
     const u32 kthr_l = window_key(octave_of(f_of_key(kmx)) - kWindow);
     u32 below;
-    const u32 total = emit_region<DT, false>(a, row, blk, start, end, kz, kthr_l, 1.0f, sc, &below);
+    const u32 total = emit_region<DT, false>(a, row, blk, start, kz, kthr_l, 1.0f, lds, sc, &below);
     QS_TR(2);
     if (tid == 0) {
       const bool fits = total <= (u32)a.R;
@@ -2269,42 +2432,52 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
     const int N = octave_of(f_of_key(rkmax));
     // a timed-out barrier, or a peaked row: k_finish resolves it
     if ((st & kStTimeout) || (!(st & kStOverflow) && candn <= (u32)kFinCap)) return;
-    // ---- flat row: exact weights, per-bin masses of this chunk
-    const double yhi = y_of(f_of_key(rkmax));
+    // ---- flat row: exact weights, kept packed in registers; the chunk's mass,
+    // its bin masses (high 32-bit parts) and, without top-p, its segment masses
+    const float qhi = f_of_key(rkmax);
+    const double yhi = y_of(qhi);
     double ylo = rnkmin ? y_of(f_of_key(~rnkmin)) : yhi;
     if (ylo < (double)(N - kWindow)) ylo = (double)(N - kWindow);
-    const double bscale = (yhi > ylo) ? (double)kBins / (yhi - ylo) : 0.0;
-    u64* blo_m = (u64*)lds;          // [kBins] low 32-bit parts of the bin masses
-    u64* bhi_m = blo_m + kBins;      // [kBins] high parts
-    u64* gmh = bhi_m + kBins;        // [kBins] the row's histogram, read back
-    blo_m[tid] = 0ull;
-    bhi_m[tid] = 0ull;
+    const QBins qb = qbins_of((float)(ylo / kLog2e), qhi);
+    u64* bh = (u64*)lds;        // [kBins] sums of w >> 32 per bin
+    u64* gmh = bh + kBins;      // [kBins] the row's histogram, read back
+    bh[tid] = 0ull;
     __syncthreads();
-    u128 acc = 0;
+    u64 vlo[NV];
+    u32 vhi[NV];
 #pragma unroll
-    for (int i = 0; i < kEPT; ++i) {
-      u32 ki = kz[i];
-      asm volatile("" : "+v"(ki));
-      const double y = y_of(f_of_key(ki));
-      const u64 w = ki ? weight_y(y, N) : 0ull;
-      if (w) {
-        acc += (u128)w;
-        if (p.topp_on) {
-          const int b = mass_bin(y, ylo, bscale);
-          atomicAdd(&blo_m[b], w & 0xffffffffull);
-          atomicAdd(&bhi_m[b], w >> 32);
-        }
+    for (int v = 0; v < NV; ++v) {
+      vlo[v] = 0ull;
+      vhi[v] = 0u;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        const int i = v * VW + j;
+        u32 ki = kz[i];
+        asm volatile("" : "+v"(ki));
+        const float q = f_of_key(ki);
+        const u64 w = ki ? wunpack(wpack(q, N)) : 0ull;
+        vlo[v] += w;
+        vhi[v] += vlo[v] < w ? 1u : 0u;
+        if (p.topp_on && (w >> 32)) atomicAdd(&bh[qb.bin(q)], w >> 32);
       }
     }
-    acc = block_sum128(acc, sc);  // its barriers also order the LDS atomics
+    u128 tsum = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) tsum += mk128(vlo[v], vhi[v]);
+    const u128 acc = block_sum128(tsum, sc);  // its barriers also order the LDS atomics
     if (tid == 0) {
       stc(&slots[blk].s_lo, (u64)acc);
       stc(&slots[blk].s_hi, (u64)(acc >> 64));
     }
     QS_TR(5);
-    if (!p.topp_on) return;  // plain draw: k_finish finds the chunk and the token
+    u64* sgm = a.segm + ((size_t)row * a.G + blk) * (2 * kSegs);
+    if (!p.topp_on) {
+      // plain draw: the segment masses let k_finish find the token
+      store_segments<NV>(sgm, vlo, vhi);
+      return;
+    }
     u64* gh = a.mhist + (size_t)row * kBins;
-    if (bhi_m[tid]) addc(&gh[tid], bhi_m[tid]);
+    if (bh[tid]) addc(&gh[tid], bh[tid]);
     row_barrier(c, (u32)a.G, 2u);
     QS_TR(6);
     // every workgroup: the total mass, the target and the bracket of bins
@@ -2320,74 +2493,137 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
       stc(&c->tp_hi, (u64)(Tp >> 64));
       stc(&c->flat_blo, (u32)blo);
     }
-    // this chunk: exact mass above the bracket; its bracketed tokens,
-    // aggregated by key, appended to the row's list as (key, chunk, count)
-    const u128 av = (tid > bhi) ? mk128(blo_m[tid], 0) + ((u128)bhi_m[tid] << 32) : (u128)0;
-    const u128 above = block_sum128(av, sc);
-    u32* stg = (u32*)(gmh + kBins);  // [kHash] keys of the bracketed tokens
-    u32* hk = stg + kHash;           // [kHash] hash table: key
-    u32* hc = hk + kHash;            //                     count
+    const u32 kwin = window_key(N - kWindow);  // the tokens with weight: keys >= kwin
+    // this chunk: exact mass above the bracket per segment; its bracketed
+    // tokens, aggregated by (key, segment), appended to the row's list.  Each
+    // wave stages its bracketed tokens in its own quarter of `stg` (ballot
+    // positions, no atomics).
+    u64* stg = (u64*)(gmh + kBins);  // [kStage2] key << 32 | segment + 1
+    u64* hk = stg + kStage2;         // [kHash] hash table: key << 32 | segment + 1
+    u32* hc = (u32*)(hk + kHash);    //                     count
     for (int i = tid; i < kHash; i += kThreads) {
-      hk[i] = 0u;
+      hk[i] = 0ull;
       hc[i] = 0u;
     }
-    if (tid == 0) sc.r[13] = 0u;
-    __syncthreads();
+    constexpr u32 kQ = kStage2 / kWaves;
+    const u32 wbase = (u32)(tid >> 6) * kQ;
+    u32 run = 0u;  // this wave's bracketed tokens so far
 #pragma unroll
-    for (int i = 0; i < kEPT; ++i) {
-      u32 ki = kz[i];
-      asm volatile("" : "+v"(ki));  // recomputed here: keeping 32 doubles from the last pass costs registers
-      const double y = y_of(f_of_key(ki));
-      bool in = false;
-      if (ki && floor(y) >= (double)(N - kWindow)) {
-        const int b = mass_bin(y, ylo, bscale);
-        in = b >= blo && b <= bhi;
-      }
-      const u32 slot = wave_append(in, &sc.r[13]);
-      if (in && slot < (u32)kHash) stg[slot] = ki;
-    }
-    __syncthreads();
-    const u32 nbt = sc.r[13];
-    const u32 nst = nbt < (u32)kHash ? nbt : (u32)kHash;
-    for (u32 s = tid; s < nst; s += kThreads) {
-      const u32 key = stg[s];
-      u32 h = (key * 0x9E3779B1u) >> 22;  // kHash = 1024 slots
-      for (int probe = 0; probe < kHash; ++probe) {
-        const u32 prev = atomicCAS(&hk[h], 0u, key);
-        if (prev == 0u || prev == key) {
-          atomicAdd(&hc[h], 1u);
-          break;
+    for (int v = 0; v < NV; ++v) {
+      vlo[v] = 0ull;
+      vhi[v] = 0u;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) {
+        const int i = v * VW + j;
+        u32 ki = kz[i];
+        asm volatile("" : "+v"(ki));  // recomputed here: keeping 32 weights from the last pass costs registers
+        const float q = f_of_key(ki);
+        const int b = qb.bin(q);
+        const u64 w = (ki >= kwin && b > bhi) ? wunpack(wpack(q, N)) : 0ull;
+        vlo[v] += w;
+        vhi[v] += vlo[v] < w ? 1u : 0u;
+        const bool in = ki >= kwin && b >= blo && b <= bhi;
+        const u64 bal = __ballot(in);
+        if (bal) {
+          const u32 r = run + __builtin_amdgcn_mbcnt_hi((u32)(bal >> 32), __builtin_amdgcn_mbcnt_lo((u32)bal, 0u));
+          if (in && r < kQ) stg[wbase + r] = ((u64)ki << 32) | (u32)(v * kWaves + (tid >> 6) + 1);
+          run += (u32)__popcll(bal);
         }
-        h = (h + 1u) & (u32)(kHash - 1);
+      }
+    }
+    store_segments<NV>(sgm, vlo, vhi);
+    u128 asum = 0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) asum += mk128(vlo[v], vhi[v]);
+    if (lane_id() == 0) sc.v[tid >> 6][5] = run;  // read after block_sum128's first barrier
+    const u128 above = block_sum128(asum, sc);  // its barriers also publish the staging
+    u32 nbt = 0u, sovf = 0u;
+    for (int w = 0; w < kWaves; ++w) {
+      const u32 n = sc.v[w][5];
+      nbt += n;
+      sovf |= n > kQ ? 1u : 0u;
+    }
+    for (int w = 0; w < kWaves; ++w) {
+      const u32 n = min(sc.v[w][5], kQ);
+      for (u32 t = tid; t < n; t += kThreads) {
+        const u64 hkey = stg[w * kQ + t];
+        u32 h = (((u32)(hkey >> 32)) ^ ((u32)hkey << 27)) * 0x9E3779B1u >> 22;  // kHash = 1024 slots
+        for (int probe = 0; probe < kHash; ++probe) {
+          const u64 prev = atomicCAS((unsigned long long*)&hk[h], 0ull, (unsigned long long)hkey);
+          if (prev == 0ull || prev == hkey) {
+            atomicAdd(&hc[h], 1u);
+            break;
+          }
+          h = (h + 1u) & (u32)(kHash - 1);
+        }
       }
     }
     __syncthreads();
+    // (key, segment) counts: this chunk's own list, read by k_finish for the
+    // chunk holding the draw or the boundary token
     u32 ne = 0u;
 #pragma unroll
     for (int q = 0; q < kHash / kThreads; ++q) ne += hc[tid * (kHash / kThreads) + q] ? 1u : 0u;
+    u32 nes;
+    u32 o = block_scan_u32(ne, sc, &nes);
+    const bool sfit = !sovf && nes <= (u32)kSegEnt;
+    u64* sent = a.sent + ((size_t)row * a.G + blk) * kSegEnt;
+    // then per key (the staging area becomes a second table): the row's list
+    u64* hk2 = stg;                 // [kHash] key + 1... as key << 32 | 1
+    u32* hc2 = (u32*)(hk2 + kHash); // [kHash] count
+    for (int i = tid; i < kHash; i += kThreads) {
+      hk2[i] = 0ull;
+      hc2[i] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kHash / kThreads; ++q) {
+      const int h = tid * (kHash / kThreads) + q;
+      const u32 n = hc[h];
+      if (n) {
+        const u64 hkey = hk[h];
+        const u32 key = (u32)(hkey >> 32);
+        if (sfit) sent[o++] = ((u64)key << 32) | ((((u32)hkey - 1u) & 31u) << 16) | n;
+        const u64 k2 = ((u64)key << 32) | 1u;
+        u32 h2 = (key * 0x9E3779B1u) >> 22;  // kHash = 1024 slots
+        for (int probe = 0; probe < kHash; ++probe) {
+          const u64 prev = atomicCAS((unsigned long long*)&hk2[h2], 0ull, (unsigned long long)k2);
+          if (prev == 0ull || prev == k2) {
+            atomicAdd(&hc2[h2], n);
+            break;
+          }
+          h2 = (h2 + 1u) & (u32)(kHash - 1);
+        }
+      }
+    }
+    __syncthreads();
+    u32 nk = 0u;
+#pragma unroll
+    for (int q = 0; q < kHash / kThreads; ++q) nk += hc2[tid * (kHash / kThreads) + q] ? 1u : 0u;
     u32 net;
-    const u32 neoff = block_scan_u32(ne, sc, &net);
+    const u32 neoff = block_scan_u32(nk, sc, &net);
     if (tid == 0) {
       stc(&slots[blk].a_lo, (u64)above);
       stc(&slots[blk].a_hi, (u64)(above >> 64));
       stc(&slots[blk].nbr, nbt);
-      if (nbt > (u32)kHash) orc(&c->status, kStList);
+      stc(&slots[blk].nse, sfit ? nes : 0xffffffffu);
+      if (sovf) orc(&c->status, kStList);
       sc.r[12] = net ? addc(&c->list_n, net) : 0u;
     }
     __syncthreads();
     const u32 base = sc.r[12];
-    if (net && nbt <= (u32)kHash && (u64)base + net <= (u64)kListCap) {
+    if (net && !sovf && (u64)base + net <= (u64)kListCap) {
       u64* lst = a.list + (size_t)row * kListCap + base + neoff;
-      u32 pos = 0u;
+      u32 o2 = 0u;
 #pragma unroll
       for (int q = 0; q < kHash / kThreads; ++q) {
         const int h = tid * (kHash / kThreads) + q;
-        const u32 n = hc[h];
+        const u32 n = hc2[h];
         if (n) {
-          u32* ent = (u32*)&lst[pos];
+          u32* ent = (u32*)&lst[o2];
           stc(&ent[0], ((u32)blk << 16) | n);
-          stc(&ent[1], hk[h]);
-          ++pos;
+          stc(&ent[1], (u32)(hk2[h] >> 32));
+          ++o2;
         }
       }
     }
@@ -2416,9 +2652,6 @@ __global__ __launch_bounds__(kThreads) void k_finish(Args a) {
   if (ROLE == 0) {
     if (p.kind == kGreedy || (p.kind == kMass && !(a.flags & QS_FLAG_NO_MASS_ROWS))) return;
     QS_TR(0);
-#ifdef QS_TRACE
-    if (a.trace && threadIdx.x == 0) a.trace[(size_t)sc.tslot * 16 + 1] = clock64();
-#endif
     if (p.kind == kTopK) {
       if (!finish_row<true>(a, p, row, 0u, lds, sc)) resolve_single<DT>(a, p, row, lds, sc);
     } else {
@@ -2427,9 +2660,6 @@ __global__ __launch_bounds__(kThreads) void k_finish(Args a) {
     }
     reset_row(a, row);
     QS_TR(15);
-#ifdef QS_TRACE
-    if (a.trace && threadIdx.x == 0) a.trace[(size_t)sc.tslot * 16 + 2] = clock64();
-#endif
     return;
   }
   if (p.kind != kMass) return;
@@ -2527,7 +2757,7 @@ int fail(const char* fmt, const char* detail = "") {
 
 struct Layout {
   int G, R, logR, seg_cap, Hpad;
-  size_t off_ctl, off_cand, off_hist, off_list, off_slots, total;
+  size_t off_ctl, off_cand, off_hist, off_list, off_slots, off_segm, off_sent, total;
   size_t lds_sample, lds_finish;
 };
 
@@ -2536,10 +2766,11 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 Layout layout_for(int B, int V, int H) {
   Layout L;
   L.G = (V + kCH - 1) / kCH;
-  // region capacity: the largest power of two with G * R <= kRegionTotal
+  // region capacity: the largest power of two with G * R <= kRegionTotal and
+  // R <= kStageCap (a region is staged in LDS before it is written)
   L.R = 1;
   L.logR = 0;
-  while (L.G * (L.R * 2) <= kRegionTotal) {
+  while (L.G * (L.R * 2) <= kRegionTotal && L.R * 2 <= kStageCap) {
     L.R *= 2;
     ++L.logR;
   }
@@ -2557,13 +2788,17 @@ Layout layout_for(int B, int V, int H) {
   o = align_up(o + (size_t)B * kListCap * 8, 256);
   L.off_slots = o;
   o = align_up(o + (size_t)B * L.G * sizeof(Slot), 256);
+  L.off_segm = o;
+  o = align_up(o + (size_t)B * L.G * kSegs * 16, 256);
+  L.off_sent = o;
+  o = align_up(o + (size_t)B * L.G * kSegEnt * 8, 256);
   L.total = o;
   const size_t pen = H > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 0;
-  const size_t stage = (size_t)3 * kFinCap * 4;  // finish_row's staging: ids, keys, weights
-  const size_t fin = stage > sizeof(WideLds) + 2 * sizeof(SelLds) ? stage : sizeof(WideLds) + 2 * sizeof(SelLds);
-  const size_t flat = sizeof(FlatLds);
+  const size_t fin = kHoffBytes + sizeof(WideLds) + 2 * sizeof(SelLds);  // finish_row
+  const size_t flat = sizeof(FlatLds) + pen;  // the penalty table follows FlatLds
   const size_t single = sizeof(SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
-  const size_t bins = (size_t)3 * kBins * 8 + (size_t)3 * kHash * 4;  // flat mass rows in k_sample
+  size_t bins = (size_t)2 * kBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
+  if ((size_t)L.R * 8 > bins) bins = (size_t)L.R * 8;                // region staging
   L.lds_sample = pen > bins ? pen : bins;
   L.lds_finish = pen;
   if (fin > L.lds_finish) L.lds_finish = fin;
@@ -2668,6 +2903,8 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   a.mhist = (u64*)(base + L.off_hist);
   a.list = (u64*)(base + L.off_list);
   a.slots = (Slot*)(base + L.off_slots);
+  a.segm = (u64*)(base + L.off_segm);
+  a.sent = (u64*)(base + L.off_sent);
 #ifdef QS_TRACE
   a.trace = g_trace;
 #endif
