@@ -39,3 +39,12 @@ def run_gpu(w, device, step=0, want_probs=True, all_greedy=False, use_top_p=True
 
 def run_oracle(w, step=0, want_probs=True):
     return contract.sample_workload(w, step=step, want_probs=want_probs)
+
+
+# Per-row resolution record of the last call, from the row control blocks at
+# the start of the workspace (256 bytes per row): word 30 is the path (0
+# greedy, 1 top-k, 2 flat mass row, 3 single workgroup, 4 peaked mass row),
+# word 32 the reason a row went to the single-workgroup path (0: it did not).
+def row_paths(ws, B):
+    raw = ws.buf[: B * 256].cpu().numpy().view(np.uint32).reshape(B, 64)
+    return raw[:, 30].copy(), raw[:, 32].copy()
