@@ -60,6 +60,8 @@ constexpr int kStageCap = 1024;                   // region entries staged in LD
 constexpr int kHoffBytes = 2048;                  // finish_row: region offsets ahead of the histogram
 constexpr int kFinCap = 4096;                     // region entries gathered per row; bracket entries per row
 constexpr int kSmallMax = 256;                    // finish_small: members, one per thread
+constexpr int kSmallPre = 64;                     // top-k rows with more members are pre-filtered
+constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample                    // finish_small: members, one per thread
 constexpr int kBins = 256;                        // histogram bins
 constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
 constexpr int kWide = 1 << kWideBits;
@@ -198,6 +200,15 @@ __device__ __forceinline__ T addc(T* p, T v) {
 template <typename T>
 __device__ __forceinline__ T maxc(T* p, T v) {
   return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A 16-byte entry as two device-coherent 8-byte accesses.
+__device__ __forceinline__ void stc_u4(uint4* p, uint4 v) {
+  stc((u64*)p, ((u64)v.y << 32) | v.x);
+  stc((u64*)p + 1, ((u64)v.w << 32) | v.z);
+}
+__device__ __forceinline__ uint4 ldc_u4(const uint4* p) {
+  const u64 a = ldc((const u64*)p), b = ldc((const u64*)p + 1);
+  return make_uint4((u32)a, (u32)(a >> 32), (u32)b, (u32)(b >> 32));
 }
 __device__ __forceinline__ void orc(u32* p, u32 v) {
   __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -439,13 +450,18 @@ Layout layout_for(int B, int V, int H) {
   return L;
 }
 
-// k_sample then, unless every row is greedy, k_finish, on one stream.  The
-// streaming pass of greedy and top-k rows and the finishing kernels run
-// 256-thread workgroups, the mass rows' streaming pass 1024-thread ones.
+// k_sample then, unless every row is greedy, k_finish, on one stream; with
+// `fused` (small batches) k_sample's last workgroup of each row finishes it
+// instead, which saves the second launch.  256-thread workgroups.
 template <int DT, int ROLE>
-hipError_t launch_role(const Args& a, const Layout& L, bool finish, hipStream_t st) {
-  hipLaunchKernelGGL((w256::k_sample<DT, ROLE>), dim3(a.G, a.B), dim3(256), ROLE == 0 ? L.lds_sample0 : L.lds_sample1,
-                     st, a);
+hipError_t launch_role(const Args& a, const Layout& L, bool finish, bool fused, hipStream_t st) {
+  const size_t lds = ROLE == 0 ? L.lds_sample0 : L.lds_sample1;
+  if (fused) {
+    hipLaunchKernelGGL((w256::k_sample<DT, ROLE, true>), dim3(a.G, a.B), dim3(256),
+                       lds > L.lds_finish ? lds : L.lds_finish, st, a);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((w256::k_sample<DT, ROLE, false>), dim3(a.G, a.B), dim3(256), lds, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !finish) return e;
   hipLaunchKernelGGL((w256::k_finish<DT, ROLE>), dim3(a.B), dim3(256), L.lds_finish, st, a);
@@ -545,6 +561,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
 #endif
 
   const bool mass = !(flags & (QS_FLAG_ALL_GREEDY | QS_FLAG_NO_MASS_ROWS));
+  const bool fused = B <= kFusedMaxB;
   SideStream* side = nullptr;
   hipError_t e;
   if (mass) {
@@ -555,12 +572,12 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
     e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
     if (e != hipSuccess) return fail("qs_sample: fork failed: %s", hipGetErrorString(e));
-    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, side->stream)
-                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, side->stream);
+    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, fused, side->stream)
+                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, fused, side->stream);
     if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
   }
-  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, stream)
-                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, stream);
+  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, fused, stream)
+                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, fused, stream);
   if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
   if (mass) {
     e = hipEventRecord(side->join, side->stream);
