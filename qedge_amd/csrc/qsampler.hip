@@ -368,19 +368,12 @@ __device__ __forceinline__ RowParams row_params(const Args& a, int row) {
   return p;
 }
 
-// The device code at two workgroup widths: 256 threads (32 logits each) for
-// the streaming pass of greedy and top-k rows and for the finishing kernels,
-// 1024 threads (8 logits each) for the mass rows' streaming pass, whose
-// workgroups go through several row-wide phases: with fewer logits per thread
-// each phase is shorter.
+// The device code, written against the workgroup width kThreads (every
+// launch uses 256 threads: 4 waves of 64, 32 logits per thread).
 namespace w256 {
 constexpr int kThreads = 256;
 #include "qsampler_body.inc"
 }  // namespace w256
-namespace w1024 {
-constexpr int kThreads = 1024;
-#include "qsampler_body.inc"
-}  // namespace w1024
 
 __global__ void k_zero(u32* p, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -435,9 +428,9 @@ Layout layout_for(int B, int V, int H) {
   o = align_up(o + (size_t)B * L.G * kSegEnt * 8, 256);
   L.total = o;
   const size_t pen = H > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 0;
-  const size_t fin = kHoffBytes + sizeof(w1024::WideLds) + 2 * sizeof(w1024::SelLds);  // finish_row
-  const size_t flat = sizeof(w1024::FlatLds) + pen;  // the penalty table follows FlatLds
-  const size_t single = sizeof(w1024::SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
+  const size_t fin = kHoffBytes + sizeof(w256::WideLds) + 2 * sizeof(w256::SelLds);  // finish_row
+  const size_t flat = sizeof(w256::FlatLds) + pen;  // the penalty table follows FlatLds
+  const size_t single = sizeof(w256::SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
   size_t bins = (size_t)2 * kBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
   if ((size_t)L.R * 8 > bins) bins = (size_t)L.R * 8;                // region staging
   const size_t stage = (size_t)L.R * 8;  // region staging
