@@ -61,7 +61,8 @@ constexpr int kHoffBytes = 2048;                  // finish_row: region offsets 
 constexpr int kFinCap = 4096;                     // region entries gathered per row; bracket entries per row
 constexpr int kSmallMax = 256;                    // finish_small: members, one per thread
 constexpr int kSmallPre = 64;                     // top-k rows with more members are pre-filtered
-constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample                    // finish_small: members, one per thread
+constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample
+constexpr int kFusedMaxBMass = 64;                // the same for the mass-row launch (its other rows exit at once)
 constexpr int kBins = 256;                        // histogram bins
 constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
 constexpr int kWide = 1 << kWideBits;
@@ -271,6 +272,20 @@ __device__ __forceinline__ u32 wpack_y(double y, int N) {
   return ((u32)(n - N + kWindow) << 24) | mant24(exp2_poly((float)(y - fl)));
 }
 __device__ __forceinline__ u32 wpack(float q, int N) { return wpack_y(y_of(q), N); }
+// wpack without branches (selects only), so that the streaming passes can
+// interleave the fp64 chains of their 32 tokens; `valid` false gives 0.  Same
+// value as wpack for every input.
+__device__ __forceinline__ u32 wpack_nb(float q, int N, bool valid) {
+  double y = (double)q * kLog2e;
+  y = (y >= -kYClamp) ? y : -kYClamp;  // also NaN -> -kYClamp, as y_of
+  y = (y > kYClamp) ? kYClamp : y;
+  const double fl = floor(y);
+  const int n = (int)fl;
+  float pf = exp2_poly((float)(y - fl));
+  pf = fminf(fmaxf(pf, 1.0f), __uint_as_float(0x3fffffffu));  // mant24's clamps
+  const u32 wp = ((u32)(n - N + kWindow) << 24) | (0x800000u | (__float_as_uint(pf) & 0x7fffffu));
+  return (valid && n >= N - kWindow) ? wp : 0u;
+}
 __device__ __forceinline__ u64 wunpack(u32 wp) { return wp ? (u64)(wp & 0xffffffu) << (wp >> 24) : 0ull; }
 // Smallest non-NaN key whose octave floor(y) is at least n0 (keys at or above
 // it are exactly the tokens inside a window that starts at octave n0).
@@ -554,7 +569,8 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
 #endif
 
   const bool mass = !(flags & (QS_FLAG_ALL_GREEDY | QS_FLAG_NO_MASS_ROWS));
-  const bool fused = B <= kFusedMaxB;
+  const bool fused = B <= kFusedMaxB;        // greedy and top-k rows
+  const bool fused1 = B <= kFusedMaxBMass;   // mass rows
   SideStream* side = nullptr;
   hipError_t e;
   if (mass) {
@@ -565,8 +581,8 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
     e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
     if (e != hipSuccess) return fail("qs_sample: fork failed: %s", hipGetErrorString(e));
-    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, fused, side->stream)
-                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, fused, side->stream);
+    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, fused1, side->stream)
+                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, fused1, side->stream);
     if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
   }
   e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, fused, stream)
