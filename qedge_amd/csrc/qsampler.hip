@@ -442,7 +442,7 @@ Layout layout_for(int B, int V, int H) {
   L.off_sent = o;
   o = align_up(o + (size_t)B * L.G * kSegEnt * 8, 256);
   L.total = o;
-  const size_t pen = H > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 0;
+  const size_t pen = H > 0 ? (size_t)kCH * 2 : 0;  // 16-bit history counts of one chunk
   const size_t fin = kHoffBytes + sizeof(w256::WideLds) + 2 * sizeof(w256::SelLds);  // finish_row
   const size_t flat = sizeof(w256::FlatLds) + pen;  // the penalty table follows FlatLds
   const size_t single = sizeof(w256::SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
@@ -594,7 +594,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
     if (e != hipSuccess) return fail("qs_sample: join failed: %s", hipGetErrorString(e));
   }
   if (out_probs) {
-    const size_t plds = Heff > 0 ? (size_t)(2 * (kCH / 32) + L.seg_cap) * 4 : 16;
+    const size_t plds = Heff > 0 ? (size_t)kCH * 2 : 16;
     if (dtype == QS_DTYPE_F32)
       hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(256), plds, stream, a);
     else
