@@ -330,6 +330,20 @@ __device__ __forceinline__ double u128_to_double(u128 x) {
   d = d + (double)(u32)lo;
   return d;
 }
+// z / b for a row-constant b, with r = 1 / b (correctly rounded): Markstein's
+// correction of q0 = z * r by the exact residual fma(-q0, b, z).  It equals
+// the correctly rounded z / b whenever div_fast_ok holds (|z| and |q0| in
+// [2^-100, 2^100)): checked against the division for every fp32 z and 23
+// divisors from 1.2e-36 to 3.4e37, and for 1e9 random (z, b) pairs.
+__device__ __forceinline__ float div_fast(float z, float b, float r) {
+  const float q0 = z * r;
+  const float e = __builtin_fmaf(-q0, b, z);
+  return __builtin_fmaf(e, r, q0);
+}
+__device__ __forceinline__ bool div_fast_ok(float z, float r) {
+  const u32 aq = __float_as_uint(z * r) & 0x7fffffffu, az = __float_as_uint(z) & 0x7fffffffu;
+  return (aq - 0x0d800000u) < (0x71800000u - 0x0d800000u) && (az - 0x0d800000u) < (0x71800000u - 0x0d800000u);
+}
 __device__ __forceinline__ float apply_penalty(float z, u32 c, float rep, float pres, float freq) {
   z = (z > 0.0f) ? (z / rep) : (z * rep);
   const float fc = freq * (float)c;
