@@ -235,3 +235,29 @@ def test_graph_replays_match_eager(gpu):
             np.testing.assert_array_equal(outs[s].cpu().numpy(), eager[s])
         steps()  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_special_values_in_top_keys(gpu, dtype):
+    """NaN, -0 and +0 among the largest logits of top-k rows (the streaming
+    pass ranks raw z bits there), an all-equal row, a row of -inf but three
+    tokens, and more than 32 chunks per row (V = 300001)."""
+    rng = np.random.default_rng(11)
+    B, V = 8, 300001
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    top = np.argsort(-x[0])[:40]
+    x[0, top[::3]] = np.nan                  # NaN scattered through the top-40 of row 0
+    x[1] = np.minimum(x[1], 0.0)
+    x[1, rng.integers(0, V, 500)] = -0.0     # many -0 next to +0 at the top of row 1
+    x[1, rng.integers(0, V, 500)] = 0.0
+    x[2] = 1.25                              # every token tied
+    x[3] = -np.inf
+    x[3, [7, V // 2, V - 1]] = [1.0, 1.0, 0.5]
+    x[4, V - 5:] = 50.0                      # the top-k in the row's last (partial) chunk
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    T = np.array([0.9, 1.0, 0.7, 1.0, 0.5, 1.1, 0.8, 0.0], np.float32)
+    P = np.array([0.9, 0.8, 0.95, 1.0, 0.9, 0.7, 1.0, 1.0], np.float32)
+    K = np.array([30, 200, 10, 2, 3, 0, 64, 0], np.int32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] special values {dtype}", flush=True)
+    _check(xx, dtype, gpu, T, P, K, u=u)
