@@ -64,6 +64,7 @@ constexpr int kSmallPre = 64;                     // top-k rows with more member
 constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample
 constexpr int kFusedMaxBMass = 64;                // the same for the mass-row launch (its other rows exit at once)
 constexpr int kBins = 256;                        // histogram bins
+constexpr int kWBins = 1024;                      // flat mass rows: packed-weight bins
 constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
 constexpr int kWide = 1 << kWideBits;
 constexpr int kListCap = kFinCap;                 // bracket entries per row (flat mass rows)
@@ -114,7 +115,7 @@ struct __attribute__((aligned(256))) RowCtl {
   u32 kappa_p, id_p;  // kept iff key > kappa_p || (key == kappa_p && id <= id_p)
   u32 greedy;
   u32 path;        // 0 greedy, 1 top-k, 2 flat mass row, 3 single workgroup, 4 peaked mass row
-  u32 flat_blo;    // flat mass rows: lowest bin of the bracket
+  u32 flat_blo;    // flat mass rows: 1 if tokens with weight lie below the boundary's bin
   u32 why;         // why the last fallback to resolve_single was taken (kWhy*), 0 if none
   u32 pad1[31];
 };
@@ -152,7 +153,7 @@ struct Args {
   int* out_kept;
   RowCtl* ctl;
   uint4* cand; // [B, G, R] region entries {id, q key, exp2 mantissa M, octave n}
-  u64* mhist;  // [B, kBins] global mass histogram (flat mass rows)
+  u64* mhist;  // [B, kWBins] flat mass rows: the row's sums of mantissas per bin
   u64* list;   // [B, kListCap] bracket entries (key << 32 | chunk << 16 | count), flat mass rows
   u64* sent;   // [B, G, kSegEnt] per chunk: bracket entries (key << 32 | segment << 16 | count), flat mass rows
   u64* segm;   // [B, G, kSegs, 2] flat mass rows: exact mass per segment (above the bracket with top-p), lo, hi
@@ -446,7 +447,7 @@ Layout layout_for(int B, int V, int H) {
   L.off_cand = o;
   o = align_up(o + (size_t)B * L.G * L.R * 16, 256);
   L.off_hist = o;
-  o = align_up(o + (size_t)B * kBins * 8, 256);
+  o = align_up(o + (size_t)B * kWBins * 8, 256);
   L.off_list = o;
   o = align_up(o + (size_t)B * kListCap * 8, 256);
   L.off_slots = o;
@@ -460,7 +461,7 @@ Layout layout_for(int B, int V, int H) {
   const size_t fin = kHoffBytes + sizeof(w256::WideLds) + 2 * sizeof(w256::SelLds);  // finish_row
   const size_t flat = sizeof(w256::FlatLds) + pen;  // the penalty table follows FlatLds
   const size_t single = sizeof(w256::SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
-  size_t bins = (size_t)2 * kBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
+  size_t bins = (size_t)kWBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
   if ((size_t)L.R * 8 > bins) bins = (size_t)L.R * 8;                // region staging
   const size_t stage = (size_t)L.R * 8;  // region staging
   L.lds_sample0 = pen > stage ? pen : stage;
