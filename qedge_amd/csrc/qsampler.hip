@@ -589,19 +589,22 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   SideStream* side = nullptr;
   hipError_t e;
   if (mass) {
-    // the mass-row launch runs beside the other rows' launch: fork and join
-    // through events on a side stream (capturable into a HIP graph)
+    // the mass-row launch (the longer chain of the two) goes first, on the
+    // caller's stream; the other rows' launch runs beside it on a side stream,
+    // forked and joined through events (capturable into a HIP graph).  A
+    // launch behind the fork's event wait starts some microseconds later.
     side = side_stream();
     if (!side) return fail("qs_sample: no side stream (call qs_workspace_init first)%s");
     e = hipEventRecord(side->fork, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
     if (e != hipSuccess) return fail("qs_sample: fork failed: %s", hipGetErrorString(e));
-    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, fused1, side->stream)
-                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, fused1, side->stream);
+    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, fused1, stream)
+                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, fused1, stream);
     if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
   }
-  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, fused, stream)
-                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, fused, stream);
+  hipStream_t st0 = mass ? side->stream : stream;
+  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, fused, st0)
+                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, fused, st0);
   if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
   if (mass) {
     e = hipEventRecord(side->join, side->stream);
