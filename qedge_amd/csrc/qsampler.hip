@@ -50,7 +50,9 @@ typedef uint32_t u32;
 
 namespace {
 
-constexpr int kCH = 8192;                         // logits per chunk (one k_sample workgroup)
+constexpr int kCHLarge = 8192;                    // logits per chunk (one k_sample workgroup)
+constexpr int kCHSmall = 2048;                    // the same for batches of at most kSmallChunkMaxB rows
+constexpr int kSmallChunkMaxB = 8;
 constexpr int kWindow = 40;
 constexpr double kYClamp = 1073741824.0;  // 2^30
 constexpr double kLog2e = 1.4426950408889634074;
@@ -401,9 +403,17 @@ __device__ __forceinline__ RowParams row_params(const Args& a, int row) {
 // The device code, written against the workgroup width kThreads (every
 // launch uses 256 threads: 4 waves of 64, 32 logits per thread).
 namespace w256 {
+constexpr int kCH = kCHLarge;
 constexpr int kThreads = 256;
 #include "qsampler_body.inc"
 }  // namespace w256
+// Small batches: four times the workgroups per row, a quarter of the logits
+// per thread (the same code).
+namespace n2k {
+constexpr int kCH = kCHSmall;
+constexpr int kThreads = 256;
+#include "qsampler_body.inc"
+}  // namespace n2k
 
 __global__ void k_zero(u32* p, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -420,16 +430,30 @@ int fail(const char* fmt, const char* detail = "") {
 }
 
 struct Layout {
-  int G, R, logR, seg_cap, Hpad;
+  bool small;  // kCHSmall chunks (the n2k kernels)
+  int kch, G, R, logR, seg_cap, Hpad;
   size_t off_ctl, off_cand, off_hist, off_list, off_slots, off_segm, off_sent, total;
   size_t lds_sample0, lds_sample1, lds_finish;  // k_sample of greedy and top-k rows, of mass rows; k_finish
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Small batches whose rows fit kMaxChunks small chunks use them.
+bool small_chunks(int B, int V) { return B <= kSmallChunkMaxB && (V + kCHSmall - 1) / kCHSmall <= kMaxChunks; }
+
+template <typename NS_WIDE, typename NS_SEL, typename NS_FLAT, typename NS_SINGLE>
+struct LdsSizes {
+  static constexpr size_t wide = sizeof(NS_WIDE), sel = sizeof(NS_SEL), flat = sizeof(NS_FLAT),
+                          single = sizeof(NS_SINGLE);
+};
+using LdsLarge = LdsSizes<w256::WideLds, w256::SelLds, w256::FlatLds, w256::SingleLds>;
+using LdsSmall = LdsSizes<n2k::WideLds, n2k::SelLds, n2k::FlatLds, n2k::SingleLds>;
+
 Layout layout_for(int B, int V, int H) {
   Layout L;
-  L.G = (V + kCH - 1) / kCH;
+  L.small = small_chunks(B, V);
+  L.kch = L.small ? kCHSmall : kCHLarge;
+  L.G = (V + L.kch - 1) / L.kch;
   // region capacity: the largest power of two with G * R <= kRegionTotal and
   // R <= kStageCap (a region is staged in LDS before it is written)
   L.R = 1;
@@ -438,7 +462,7 @@ Layout layout_for(int B, int V, int H) {
     L.R *= 2;
     ++L.logR;
   }
-  L.seg_cap = H > 0 ? (H < kCH ? H : kCH) : 0;
+  L.seg_cap = H > 0 ? (H < L.kch ? H : L.kch) : 0;
   L.Hpad = 1;
   while (L.Hpad < H) L.Hpad <<= 1;
   size_t o = 0;
@@ -457,10 +481,12 @@ Layout layout_for(int B, int V, int H) {
   L.off_sent = o;
   o = align_up(o + (size_t)B * L.G * kSegEnt * 8, 256);
   L.total = o;
-  const size_t pen = H > 0 ? (size_t)kCH * 2 : 0;  // 16-bit history counts of one chunk
-  const size_t fin = kHoffBytes + sizeof(w256::WideLds) + 2 * sizeof(w256::SelLds);  // finish_row
-  const size_t flat = sizeof(w256::FlatLds) + pen;  // the penalty table follows FlatLds
-  const size_t single = sizeof(w256::SingleLds) + (H > 0 ? (size_t)L.Hpad * 4 : 0);
+  const size_t pen = H > 0 ? (size_t)L.kch * 2 : 0;  // 16-bit history counts of one chunk
+  const size_t swide = L.small ? LdsSmall::wide : LdsLarge::wide, ssel = L.small ? LdsSmall::sel : LdsLarge::sel;
+  const size_t sflat = L.small ? LdsSmall::flat : LdsLarge::flat, ssingle = L.small ? LdsSmall::single : LdsLarge::single;
+  const size_t fin = kHoffBytes + swide + 2 * ssel;  // finish_row
+  const size_t flat = sflat + pen;                   // the penalty table follows FlatLds
+  const size_t single = ssingle + (H > 0 ? (size_t)L.Hpad * 4 : 0);
   size_t bins = (size_t)kWBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
   if ((size_t)L.R * 8 > bins) bins = (size_t)L.R * 8;                // region staging
   const size_t stage = (size_t)L.R * 8;  // region staging
@@ -480,14 +506,23 @@ template <int DT, int ROLE>
 hipError_t launch_role(const Args& a, const Layout& L, bool finish, bool fused, hipStream_t st) {
   const size_t lds = ROLE == 0 ? L.lds_sample0 : L.lds_sample1;
   if (fused) {
-    hipLaunchKernelGGL((w256::k_sample<DT, ROLE, true>), dim3(a.G, a.B), dim3(256),
-                       lds > L.lds_finish ? lds : L.lds_finish, st, a);
+    const size_t lf = lds > L.lds_finish ? lds : L.lds_finish;
+    if (L.small)
+      hipLaunchKernelGGL((n2k::k_sample<DT, ROLE, true>), dim3(a.G, a.B), dim3(256), lf, st, a);
+    else
+      hipLaunchKernelGGL((w256::k_sample<DT, ROLE, true>), dim3(a.G, a.B), dim3(256), lf, st, a);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((w256::k_sample<DT, ROLE, false>), dim3(a.G, a.B), dim3(256), lds, st, a);
+  if (L.small)
+    hipLaunchKernelGGL((n2k::k_sample<DT, ROLE, false>), dim3(a.G, a.B), dim3(256), lds, st, a);
+  else
+    hipLaunchKernelGGL((w256::k_sample<DT, ROLE, false>), dim3(a.G, a.B), dim3(256), lds, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !finish) return e;
-  hipLaunchKernelGGL((w256::k_finish<DT, ROLE>), dim3(a.B), dim3(256), L.lds_finish, st, a);
+  if (L.small)
+    hipLaunchKernelGGL((n2k::k_finish<DT, ROLE>), dim3(a.B), dim3(256), L.lds_finish, st, a);
+  else
+    hipLaunchKernelGGL((w256::k_finish<DT, ROLE>), dim3(a.B), dim3(256), L.lds_finish, st, a);
   return hipGetLastError();
 }
 
@@ -539,7 +574,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   if (H > kMaxHistory) return fail("qs_sample: history longer than QS_MAX_HISTORY%s");
   if (out_kept && !out_probs) return fail("qs_sample: out_kept requires out_probs%s");
   const int Heff = hist ? H : 0;
-  if ((V + kCH - 1) / kCH > kMaxChunks) return fail("qs_sample: V too large for the chunking%s");
+  if ((V + kCHLarge - 1) / kCHLarge > kMaxChunks) return fail("qs_sample: V too large for the chunking%s");
   const Layout L = layout_for(B, V, Heff);
   if (ws_bytes < L.total) return fail("qs_sample: workspace too small (see qs_workspace_bytes)%s");
   if (((uintptr_t)ws) % 256) return fail("qs_sample: workspace must be 256-byte aligned%s");
@@ -612,11 +647,18 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
     if (e != hipSuccess) return fail("qs_sample: join failed: %s", hipGetErrorString(e));
   }
   if (out_probs) {
-    const size_t plds = Heff > 0 ? (size_t)kCH * 2 : 16;
-    if (dtype == QS_DTYPE_F32)
-      hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(256), plds, stream, a);
-    else
-      hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_BF16>, dim3(a.G, B), dim3(256), plds, stream, a);
+    const size_t plds = Heff > 0 ? (size_t)L.kch * 2 : 16;
+    if (L.small) {
+      if (dtype == QS_DTYPE_F32)
+        hipLaunchKernelGGL(n2k::k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(256), plds, stream, a);
+      else
+        hipLaunchKernelGGL(n2k::k_probs<QS_DTYPE_BF16>, dim3(a.G, B), dim3(256), plds, stream, a);
+    } else {
+      if (dtype == QS_DTYPE_F32)
+        hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(256), plds, stream, a);
+      else
+        hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_BF16>, dim3(a.G, B), dim3(256), plds, stream, a);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return fail("qs_sample: probs kernel launch failed: %s", hipGetErrorString(e));
   }

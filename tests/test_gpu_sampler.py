@@ -9,7 +9,7 @@ from qedge_amd import workloads as W
 from qedge_amd.batch import SamplingBatch
 from qedge_amd.sampler import BatchSampler, Workspace, argmax_into, sample_gpu, sample_into
 from qedge_amd.sampling_params import SamplingParams
-from tests.devrun import run_gpu, run_oracle
+from tests.devrun import row_paths, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -28,7 +28,7 @@ def _dev_logits(x, dtype, device, stride=None):
 
 
 def _run(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hist=None, u=None,
-         use_top_p=True, mass_rows=True, stride=None, probs=True):
+         use_top_p=True, mass_rows=True, stride=None, probs=True, paths=None):
     B, V = x.shape
     lg = _dev_logits(x, dtype, device, stride)
     t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)
@@ -42,6 +42,8 @@ def _run(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hi
                 frequency_penalties=t(freq, torch.float32), history=t(hist, torch.int32),
                 uniforms=t(u, torch.float32), use_top_p=use_top_p, mass_rows=mass_rows, out_probs=pr, out_kept=kept)
     torch.cuda.synchronize()
+    if paths is not None:
+        paths.extend(row_paths(ws, B))
     return ids.cpu().numpy(), None if pr is None else pr.cpu().numpy(), None if kept is None else kept.cpu().numpy()
 
 
@@ -261,3 +263,30 @@ def test_special_values_in_top_keys(gpu, dtype):
     u = rng.random(B).astype(np.float32)
     print(f"[edge] special values {dtype}", flush=True)
     _check(xx, dtype, gpu, T, P, K, u=u)
+
+
+@pytest.mark.parametrize("B,V,dtype", [(1, 248320, "bf16"), (2, 2048 * 7 + 100, "bf16"), (3, 600001, "bf16"),
+                                       (12, 8192 * 5 + 300, "f32")])
+def test_chunk_layouts_and_sparse_last_chunks(gpu, B, V, dtype):
+    """Batches of up to 8 rows use 2048-logit chunks unless V needs more than
+    256 of them; larger batches use 8192.  A last chunk holding fewer logits
+    than one wave's share leaves waves without tokens; every row must still
+    be resolved on its fast path (no single-workgroup fallback)."""
+    rng = np.random.default_rng(B * 1000 + V % 997)
+    x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+    x[0, V - 7] = 9.0  # a top token inside the last chunk
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    kinds = [(0.8, 0.9, 20), (1.0, 0.95, 0), (0.0, 1.0, 0), (0.7, 1.0, 300), (1.2, 0.8, 5), (0.9, 0.9, 64)]
+    T = np.array([kinds[r % len(kinds)][0] for r in range(B)], np.float32)
+    P = np.array([kinds[r % len(kinds)][1] for r in range(B)], np.float32)
+    K = np.array([kinds[r % len(kinds)][2] for r in range(B)], np.int32)
+    hist = (rng.integers(0, V, (B, 512))).astype(np.int32)
+    rep = np.full(B, 1.1, np.float32)
+    pres = np.full(B, 0.2, np.float32)
+    freq = np.full(B, 0.1, np.float32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] chunk layout B={B} V={V} {dtype}", flush=True)
+    paths = []
+    _check(xx, dtype, gpu, T, P, K, rep, pres, freq, hist, u=u, probs=False, paths=paths)
+    why = paths[1]
+    assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
