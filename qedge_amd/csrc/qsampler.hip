@@ -5,10 +5,13 @@
 // greedy argmax sites (src/compute/model_runner.py:85,353).  The arithmetic
 // contract is stated in include/qsampler.h; ids are exact integers.
 //
-// Grid (G chunks, B rows), 256 threads (4 waves of 64); each workgroup streams
-// one chunk of 8192 logits of a row into registers once (16-byte loads) and
-// applies the history penalties from an LDS table.  Two launches run side by
-// side (the second on a side stream):
+// Grid (G chunks, B rows); each workgroup streams one chunk of 8192 logits of
+// a row (2048 in batches of at most 8 rows) into registers once (16-byte
+// loads) and applies the history penalties from an LDS table.  The greedy and
+// top-k rows' streaming pass runs 256 threads (4 waves of 64, 32 logits per
+// thread); the latency-bound launches (the top-k finisher, and the mass rows
+// in batches of at most 64 rows) run the same code at 512 threads.  Two
+// launches run side by side (one on a side stream):
 //   main launch  greedy rows: local argmax, one 64-bit atomic max per
 //                workgroup, the last workgroup to arrive publishes the id.
 //                top-k rows (0 < k <= QS_TOPK_FAST_MAX): every workgroup
@@ -64,7 +67,7 @@ constexpr int kFinCap = 4096;                     // region entries gathered per
 constexpr int kSmallMax = 256;                    // finish_small: members, one per thread
 constexpr int kSmallPre = 64;                     // top-k rows with more members are pre-filtered
 constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample
-constexpr int kFusedMaxBMass = 64;                // the same for the mass-row launch (its other rows exit at once)
+constexpr int kFusedMaxBMass = 64;                // the same for the mass-row launch (its grid rows are the mass rows)
 constexpr int kBins = 256;                        // histogram bins
 constexpr int kWBins = 1024;                      // flat mass rows: packed-weight bins
 constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
@@ -414,6 +417,14 @@ constexpr int kCH = kCHSmall;
 constexpr int kThreads = 256;
 #include "qsampler_body.inc"
 }  // namespace n2k
+// The same chunks as w256 with twice the threads (16 logits per thread), for
+// launches with few busy workgroups per row, whose phases are latency chains:
+// the mass rows' cooperative passes and the one-workgroup-per-row finishers.
+namespace w512 {
+constexpr int kCH = kCHLarge;
+constexpr int kThreads = 512;
+#include "qsampler_body.inc"
+}  // namespace w512
 
 __global__ void k_zero(u32* p, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -429,11 +440,17 @@ int fail(const char* fmt, const char* detail = "") {
   return -1;
 }
 
+// Device-code builds: chunk size and workgroup width.
+enum Ns : int { kNsW256 = 0, kNsN2K = 1, kNsW512 = 2 };
+constexpr int ns_threads(int ns) { return ns == kNsW512 ? 512 : 256; }
+
 struct Layout {
   bool small;  // kCHSmall chunks (the n2k kernels)
   int kch, G, R, logR, seg_cap, Hpad;
   size_t off_ctl, off_cand, off_hist, off_list, off_slots, off_segm, off_sent, total;
-  size_t lds_sample0, lds_sample1, lds_finish;  // k_sample of greedy and top-k rows, of mass rows; k_finish
+  size_t lds_sample0, lds_sample1;  // k_sample of greedy and top-k rows, of mass rows
+  int ns_sample[2], ns_finish[2];  // builds of k_sample and k_finish, per role
+  size_t lds_finish[3];                   // k_finish (and a fused k_sample's tail), per build
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -448,6 +465,21 @@ struct LdsSizes {
 };
 using LdsLarge = LdsSizes<w256::WideLds, w256::SelLds, w256::FlatLds, w256::SingleLds>;
 using LdsSmall = LdsSizes<n2k::WideLds, n2k::SelLds, n2k::FlatLds, n2k::SingleLds>;
+using LdsW512 = LdsSizes<w512::WideLds, w512::SelLds, w512::FlatLds, w512::SingleLds>;
+
+// LDS of the finishing code of build `ns` (finish_row, resolve_flat,
+// resolve_single), with `pen` bytes of penalty table and a history of Hpad ids.
+template <typename LS>
+size_t finish_lds(size_t pen, int H, int Hpad) {
+  const size_t fin = kHoffBytes + LS::wide + 2 * LS::sel;  // finish_row
+  const size_t flat = LS::flat + pen;                      // the penalty table follows FlatLds
+  const size_t single = LS::single + (H > 0 ? (size_t)Hpad * 4 : 0);
+  size_t r = pen;
+  if (fin > r) r = fin;
+  if (flat > r) r = flat;
+  if (single > r) r = single;
+  return r;
+}
 
 Layout layout_for(int B, int V, int H) {
   Layout L;
@@ -482,21 +514,54 @@ Layout layout_for(int B, int V, int H) {
   o = align_up(o + (size_t)B * L.G * kSegEnt * 8, 256);
   L.total = o;
   const size_t pen = H > 0 ? (size_t)L.kch * 2 : 0;  // 16-bit history counts of one chunk
-  const size_t swide = L.small ? LdsSmall::wide : LdsLarge::wide, ssel = L.small ? LdsSmall::sel : LdsLarge::sel;
-  const size_t sflat = L.small ? LdsSmall::flat : LdsLarge::flat, ssingle = L.small ? LdsSmall::single : LdsLarge::single;
-  const size_t fin = kHoffBytes + swide + 2 * ssel;  // finish_row
-  const size_t flat = sflat + pen;                   // the penalty table follows FlatLds
-  const size_t single = ssingle + (H > 0 ? (size_t)L.Hpad * 4 : 0);
+  L.lds_finish[kNsW256] = finish_lds<LdsLarge>(pen, H, L.Hpad);
+  L.lds_finish[kNsN2K] = finish_lds<LdsSmall>(pen, H, L.Hpad);
+  L.lds_finish[kNsW512] = finish_lds<LdsW512>(pen, H, L.Hpad);
+  // Small batches: small chunks throughout.  Otherwise the streaming pass of
+  // the greedy and top-k rows keeps 32 logits per thread (many workgroups,
+  // loads in flight), while the top-k finisher (one workgroup per row) and,
+  // in batches of at most kFusedMaxBMass rows, the mass rows' cooperative
+  // passes run twice as many threads.  Larger batches of mass rows fill the
+  // chip with 256-thread workgroups.
+  const bool wide_mass = B <= kFusedMaxBMass;
+  L.ns_sample[0] = L.small ? kNsN2K : kNsW256;
+  L.ns_sample[1] = L.small ? kNsN2K : (wide_mass ? kNsW512 : kNsW256);
+  L.ns_finish[0] = L.small ? kNsN2K : kNsW512;
+  L.ns_finish[1] = L.small ? kNsN2K : (wide_mass ? kNsW512 : kNsW256);
   size_t bins = (size_t)kWBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
   if ((size_t)L.R * 8 > bins) bins = (size_t)L.R * 8;                // region staging
   const size_t stage = (size_t)L.R * 8;  // region staging
   L.lds_sample0 = pen > stage ? pen : stage;
   L.lds_sample1 = L.lds_sample0 > bins ? L.lds_sample0 : bins;
-  L.lds_finish = pen;
-  if (fin > L.lds_finish) L.lds_finish = fin;
-  if (flat > L.lds_finish) L.lds_finish = flat;
-  if (single > L.lds_finish) L.lds_finish = single;
   return L;
+}
+
+// The builds a launch can use: k_sample of greedy and top-k rows n2k or
+// w256; of mass rows n2k, w512 (fused) or w256; k_finish of top-k rows n2k or
+// w512, of mass rows n2k, w512 or w256.
+template <int DT, int ROLE, bool FUSED>
+const void* sample_kernel(int ns) {
+  if (ns == kNsN2K) return (const void*)n2k::k_sample<DT, ROLE, FUSED>;
+  if constexpr (ROLE == 1 && FUSED) return (const void*)w512::k_sample<DT, ROLE, FUSED>;
+  return (const void*)w256::k_sample<DT, ROLE, FUSED>;
+}
+template <int DT, int ROLE>
+const void* finish_kernel(int ns) {
+  if (ns == kNsN2K) return (const void*)n2k::k_finish<DT, ROLE>;
+  if constexpr (ROLE == 1) {
+    if (ns == kNsW256) return (const void*)w256::k_finish<DT, ROLE>;
+  }
+  return (const void*)w512::k_finish<DT, ROLE>;
+}
+template <int DT>
+const void* probs_kernel(int ns) {
+  if (ns == kNsN2K) return (const void*)n2k::k_probs<DT>;
+  return (const void*)w256::k_probs<DT>;
+}
+
+hipError_t launch(const void* fn, dim3 grid, int ns, size_t lds, hipStream_t st, const Args& a) {
+  void* args[] = {(void*)&a};
+  return hipLaunchKernel(fn, grid, dim3(ns_threads(ns)), args, lds, st);
 }
 
 // k_sample then, unless every row is greedy, k_finish, on one stream; with
@@ -505,25 +570,15 @@ Layout layout_for(int B, int V, int H) {
 template <int DT, int ROLE>
 hipError_t launch_role(const Args& a, const Layout& L, bool finish, bool fused, hipStream_t st) {
   const size_t lds = ROLE == 0 ? L.lds_sample0 : L.lds_sample1;
+  const int ns = L.ns_sample[ROLE];
   if (fused) {
-    const size_t lf = lds > L.lds_finish ? lds : L.lds_finish;
-    if (L.small)
-      hipLaunchKernelGGL((n2k::k_sample<DT, ROLE, true>), dim3(a.G, a.B), dim3(256), lf, st, a);
-    else
-      hipLaunchKernelGGL((w256::k_sample<DT, ROLE, true>), dim3(a.G, a.B), dim3(256), lf, st, a);
-    return hipGetLastError();
+    const size_t lf = lds > L.lds_finish[ns] ? lds : L.lds_finish[ns];
+    return launch(sample_kernel<DT, ROLE, true>(ns), dim3(a.G, a.B), ns, lf, st, a);
   }
-  if (L.small)
-    hipLaunchKernelGGL((n2k::k_sample<DT, ROLE, false>), dim3(a.G, a.B), dim3(256), lds, st, a);
-  else
-    hipLaunchKernelGGL((w256::k_sample<DT, ROLE, false>), dim3(a.G, a.B), dim3(256), lds, st, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch(sample_kernel<DT, ROLE, false>(ns), dim3(a.G, a.B), ns, lds, st, a);
   if (e != hipSuccess || !finish) return e;
-  if (L.small)
-    hipLaunchKernelGGL((n2k::k_finish<DT, ROLE>), dim3(a.B), dim3(256), L.lds_finish, st, a);
-  else
-    hipLaunchKernelGGL((w256::k_finish<DT, ROLE>), dim3(a.B), dim3(256), L.lds_finish, st, a);
-  return hipGetLastError();
+  const int nf = L.ns_finish[ROLE];
+  return launch(finish_kernel<DT, ROLE>(nf), dim3(a.B), nf, L.lds_finish[nf], st, a);
 }
 
 #ifdef QS_TRACE
@@ -580,7 +635,8 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   if (((uintptr_t)ws) % 256) return fail("qs_sample: workspace must be 256-byte aligned%s");
   const bool all_greedy = (flags & QS_FLAG_ALL_GREEDY) != 0;
   if (!all_greedy && !uniforms) return fail("qs_sample: uniforms required unless all rows are greedy%s");
-  if (L.lds_sample1 > 64 * 1024 || L.lds_finish > 64 * 1024) return fail("qs_sample: LDS budget exceeded%s");
+  for (int ns = 0; ns < 3; ++ns)
+    if (L.lds_sample1 > 64 * 1024 || L.lds_finish[ns] > 64 * 1024) return fail("qs_sample: LDS budget exceeded%s");
 
   Args a;
   memset(&a, 0, sizeof(a));
@@ -648,18 +704,9 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   }
   if (out_probs) {
     const size_t plds = Heff > 0 ? (size_t)L.kch * 2 : 16;
-    if (L.small) {
-      if (dtype == QS_DTYPE_F32)
-        hipLaunchKernelGGL(n2k::k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(256), plds, stream, a);
-      else
-        hipLaunchKernelGGL(n2k::k_probs<QS_DTYPE_BF16>, dim3(a.G, B), dim3(256), plds, stream, a);
-    } else {
-      if (dtype == QS_DTYPE_F32)
-        hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_F32>, dim3(a.G, B), dim3(256), plds, stream, a);
-      else
-        hipLaunchKernelGGL(w256::k_probs<QS_DTYPE_BF16>, dim3(a.G, B), dim3(256), plds, stream, a);
-    }
-    e = hipGetLastError();
+    const int pns = L.small ? kNsN2K : kNsW256;
+    e = launch(dtype == QS_DTYPE_F32 ? probs_kernel<QS_DTYPE_F32>(pns) : probs_kernel<QS_DTYPE_BF16>(pns),
+               dim3(a.G, B), pns, plds, stream, a);
     if (e != hipSuccess) return fail("qs_sample: probs kernel launch failed: %s", hipGetErrorString(e));
   }
   return 0;
