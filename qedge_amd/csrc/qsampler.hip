@@ -67,7 +67,7 @@ constexpr int kFinCap = 4096;                     // region entries gathered per
 constexpr int kSmallMax = 256;                    // finish_small: members, one per thread
 constexpr int kSmallPre = 64;                     // top-k rows with more members are pre-filtered
 constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample
-constexpr int kFusedMaxBMass = 64;                // the same for the mass-row launch (its grid rows are the mass rows)
+constexpr int kOneLaunchMaxB = 64;                // batches up to this size with mass rows: one k_sample_all launch
 constexpr int kBins = 256;                        // histogram bins
 constexpr int kWBins = 1024;                      // flat mass rows: packed-weight bins
 constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
@@ -517,17 +517,15 @@ Layout layout_for(int B, int V, int H) {
   L.lds_finish[kNsW256] = finish_lds<LdsLarge>(pen, H, L.Hpad);
   L.lds_finish[kNsN2K] = finish_lds<LdsSmall>(pen, H, L.Hpad);
   L.lds_finish[kNsW512] = finish_lds<LdsW512>(pen, H, L.Hpad);
-  // Small batches: small chunks throughout.  Otherwise the streaming pass of
-  // the greedy and top-k rows keeps 32 logits per thread (many workgroups,
-  // loads in flight), while the top-k finisher (one workgroup per row) and,
-  // in batches of at most kFusedMaxBMass rows, the mass rows' cooperative
-  // passes run twice as many threads.  Larger batches of mass rows fill the
-  // chip with 256-thread workgroups.
-  const bool wide_mass = B <= kFusedMaxBMass;
+  // Builds of the per-role launches (batches with mass rows of at most
+  // kOneLaunchMaxB rows use k_sample_all instead).  Small batches: small
+  // chunks throughout.  Otherwise the streaming passes keep 32 logits per
+  // thread (many workgroups, loads in flight), while the top-k finisher (one
+  // workgroup per row) runs twice as many threads.
   L.ns_sample[0] = L.small ? kNsN2K : kNsW256;
-  L.ns_sample[1] = L.small ? kNsN2K : (wide_mass ? kNsW512 : kNsW256);
+  L.ns_sample[1] = L.small ? kNsN2K : kNsW256;
   L.ns_finish[0] = L.small ? kNsN2K : kNsW512;
-  L.ns_finish[1] = L.small ? kNsN2K : (wide_mass ? kNsW512 : kNsW256);
+  L.ns_finish[1] = L.small ? kNsN2K : kNsW256;
   size_t bins = (size_t)kWBins * 8 + (size_t)kStage2 * 8 + (size_t)kHash * (8 + 4);  // flat mass rows in k_sample
   if ((size_t)L.R * 8 > bins) bins = (size_t)L.R * 8;                // region staging
   const size_t stage = (size_t)L.R * 8;  // region staging
@@ -536,22 +534,18 @@ Layout layout_for(int B, int V, int H) {
   return L;
 }
 
-// The builds a launch can use: k_sample of greedy and top-k rows n2k or
-// w256; of mass rows n2k, w512 (fused) or w256; k_finish of top-k rows n2k or
-// w512, of mass rows n2k, w512 or w256.
+// The builds a per-role launch can use: k_sample n2k or w256; k_finish of
+// top-k rows n2k or w512, of mass rows n2k or w256.
 template <int DT, int ROLE, bool FUSED>
 const void* sample_kernel(int ns) {
   if (ns == kNsN2K) return (const void*)n2k::k_sample<DT, ROLE, FUSED>;
-  if constexpr (ROLE == 1 && FUSED) return (const void*)w512::k_sample<DT, ROLE, FUSED>;
   return (const void*)w256::k_sample<DT, ROLE, FUSED>;
 }
 template <int DT, int ROLE>
 const void* finish_kernel(int ns) {
   if (ns == kNsN2K) return (const void*)n2k::k_finish<DT, ROLE>;
-  if constexpr (ROLE == 1) {
-    if (ns == kNsW256) return (const void*)w256::k_finish<DT, ROLE>;
-  }
-  return (const void*)w512::k_finish<DT, ROLE>;
+  if constexpr (ROLE == 1) return (const void*)w256::k_finish<DT, ROLE>;
+  else return (const void*)w512::k_finish<DT, ROLE>;
 }
 template <int DT>
 const void* probs_kernel(int ns) {
@@ -571,9 +565,11 @@ template <int DT, int ROLE>
 hipError_t launch_role(const Args& a, const Layout& L, bool finish, bool fused, hipStream_t st) {
   const size_t lds = ROLE == 0 ? L.lds_sample0 : L.lds_sample1;
   const int ns = L.ns_sample[ROLE];
-  if (fused) {
-    const size_t lf = lds > L.lds_finish[ns] ? lds : L.lds_finish[ns];
-    return launch(sample_kernel<DT, ROLE, true>(ns), dim3(a.G, a.B), ns, lf, st, a);
+  if constexpr (ROLE == 0) {  // mass rows are fused only inside k_sample_all
+    if (fused) {
+      const size_t lf = lds > L.lds_finish[ns] ? lds : L.lds_finish[ns];
+      return launch(sample_kernel<DT, ROLE, true>(ns), dim3(a.G, a.B), ns, lf, st, a);
+    }
   }
   hipError_t e = launch(sample_kernel<DT, ROLE, false>(ns), dim3(a.G, a.B), ns, lds, st, a);
   if (e != hipSuccess || !finish) return e;
@@ -610,6 +606,38 @@ int init_side_stream() {
   if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess) return -1;
   if (hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) return -1;
   g_side_ok[dev] = true;
+  return 0;
+}
+
+// The mass rows on the caller's stream beside the other rows on the side
+// stream (fork and join through events), or the other rows alone.
+int launch_two(const Args& a, const Layout& L, int dtype, bool mass, bool fused, bool all_greedy,
+               hipStream_t stream) {
+  SideStream* side = nullptr;
+  hipError_t e;
+  if (mass) {
+    // the mass-row launch (the longer chain of the two) goes first, on the
+    // caller's stream; the other rows' launch runs beside it on a side stream,
+    // forked and joined through events (capturable into a HIP graph).  A
+    // launch behind the fork's event wait starts some microseconds later.
+    side = side_stream();
+    if (!side) return fail("qs_sample: no side stream (call qs_workspace_init first)%s");
+    e = hipEventRecord(side->fork, stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (e != hipSuccess) return fail("qs_sample: fork failed: %s", hipGetErrorString(e));
+    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, false, stream)
+                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, false, stream);
+    if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
+  }
+  hipStream_t st0 = mass ? side->stream : stream;
+  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, fused, st0)
+                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, fused, st0);
+  if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
+  if (mass) {
+    e = hipEventRecord(side->join, side->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
+    if (e != hipSuccess) return fail("qs_sample: join failed: %s", hipGetErrorString(e));
+  }
   return 0;
 }
 
@@ -675,32 +703,34 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
 #endif
 
   const bool mass = !(flags & (QS_FLAG_ALL_GREEDY | QS_FLAG_NO_MASS_ROWS));
-  const bool fused = B <= kFusedMaxB;        // greedy and top-k rows
-  const bool fused1 = B <= kFusedMaxBMass;   // mass rows
-  SideStream* side = nullptr;
+  const bool fused = B <= kFusedMaxB;  // greedy and top-k rows without mass rows
+  // Batches of at most kOneLaunchMaxB rows with mass rows: one streaming
+  // launch for all rows (mass rows first in its grid), on the caller's stream.
+  // Small chunks finish the rows inside it; large chunks run it at 512
+  // threads, followed by one finishing launch for all rows.  (Two launches on
+  // two streams would overlap too, but their fork and join cost ~7 us per
+  // call inside a HIP graph.)
+  const bool one = mass && B <= kOneLaunchMaxB;
   hipError_t e;
-  if (mass) {
-    // the mass-row launch (the longer chain of the two) goes first, on the
-    // caller's stream; the other rows' launch runs beside it on a side stream,
-    // forked and joined through events (capturable into a HIP graph).  A
-    // launch behind the fork's event wait starts some microseconds later.
-    side = side_stream();
-    if (!side) return fail("qs_sample: no side stream (call qs_workspace_init first)%s");
-    e = hipEventRecord(side->fork, stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
-    if (e != hipSuccess) return fail("qs_sample: fork failed: %s", hipGetErrorString(e));
-    e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 1>(a, L, true, fused1, stream)
-                              : launch_role<QS_DTYPE_BF16, 1>(a, L, true, fused1, stream);
-    if (e != hipSuccess) return fail("qs_sample: mass kernel launch failed: %s", hipGetErrorString(e));
-  }
-  hipStream_t st0 = mass ? side->stream : stream;
-  e = dtype == QS_DTYPE_F32 ? launch_role<QS_DTYPE_F32, 0>(a, L, !all_greedy, fused, st0)
-                            : launch_role<QS_DTYPE_BF16, 0>(a, L, !all_greedy, fused, st0);
-  if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
-  if (mass) {
-    e = hipEventRecord(side->join, side->stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(stream, side->join, 0);
-    if (e != hipSuccess) return fail("qs_sample: join failed: %s", hipGetErrorString(e));
+  if (one && L.small) {
+    size_t lds = L.lds_sample0 > L.lds_sample1 ? L.lds_sample0 : L.lds_sample1;
+    if (L.lds_finish[kNsN2K] > lds) lds = L.lds_finish[kNsN2K];
+    e = launch(dtype == QS_DTYPE_F32 ? (const void*)n2k::k_sample_all<QS_DTYPE_F32, true>
+                                     : (const void*)n2k::k_sample_all<QS_DTYPE_BF16, true>,
+               dim3(a.G, B), kNsN2K, lds, stream, a);
+    if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
+  } else if (one) {
+    const size_t lds = L.lds_sample0 > L.lds_sample1 ? L.lds_sample0 : L.lds_sample1;
+    e = launch(dtype == QS_DTYPE_F32 ? (const void*)w512::k_sample_all<QS_DTYPE_F32, false>
+                                     : (const void*)w512::k_sample_all<QS_DTYPE_BF16, false>,
+               dim3(a.G, B), kNsW512, lds, stream, a);
+    if (e == hipSuccess)
+      e = launch(dtype == QS_DTYPE_F32 ? (const void*)w512::k_finish_all<QS_DTYPE_F32>
+                                       : (const void*)w512::k_finish_all<QS_DTYPE_BF16>,
+                 dim3(B), kNsW512, L.lds_finish[kNsW512], stream, a);
+    if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
+  } else {
+    if (launch_two(a, L, dtype, mass, fused, all_greedy, stream) != 0) return -1;
   }
   if (out_probs) {
     const size_t plds = Heff > 0 ? (size_t)L.kch * 2 : 16;
