@@ -68,6 +68,7 @@ constexpr int kSmallMax = 256;                    // finish_small: members, one 
 constexpr int kSmallPre = 64;                     // top-k rows with more members are pre-filtered
 constexpr int kFusedMaxB = 8;                     // batches up to this size finish rows inside k_sample
 constexpr int kOneLaunchMaxB = 64;                // batches up to this size with mass rows: one k_sample_all launch
+constexpr int kMassSlots = 8;                     // k_sample_all: grid rows for mass rows ahead of the batch's rows
 constexpr int kBins = 256;                        // histogram bins
 constexpr int kWBins = 1024;                      // flat mass rows: packed-weight bins
 constexpr int kWideBits = 11;                     // finishing histogram: 2048 bins
@@ -717,13 +718,13 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
     if (L.lds_finish[kNsN2K] > lds) lds = L.lds_finish[kNsN2K];
     e = launch(dtype == QS_DTYPE_F32 ? (const void*)n2k::k_sample_all<QS_DTYPE_F32, true>
                                      : (const void*)n2k::k_sample_all<QS_DTYPE_BF16, true>,
-               dim3(a.G, B), kNsN2K, lds, stream, a);
+               dim3(a.G, B + (B < kMassSlots ? B : kMassSlots)), kNsN2K, lds, stream, a);
     if (e != hipSuccess) return fail("qs_sample: kernel launch failed: %s", hipGetErrorString(e));
   } else if (one) {
     const size_t lds = L.lds_sample0 > L.lds_sample1 ? L.lds_sample0 : L.lds_sample1;
     e = launch(dtype == QS_DTYPE_F32 ? (const void*)w512::k_sample_all<QS_DTYPE_F32, false>
                                      : (const void*)w512::k_sample_all<QS_DTYPE_BF16, false>,
-               dim3(a.G, B), kNsW512, lds, stream, a);
+               dim3(a.G, B + (B < kMassSlots ? B : kMassSlots)), kNsW512, lds, stream, a);
     if (e == hipSuccess)
       e = launch(dtype == QS_DTYPE_F32 ? (const void*)w512::k_finish_all<QS_DTYPE_F32>
                                        : (const void*)w512::k_finish_all<QS_DTYPE_BF16>,
