@@ -5,31 +5,33 @@
 // greedy argmax sites (src/compute/model_runner.py:85,353).  The arithmetic
 // contract is stated in include/qsampler.h; ids are exact integers.
 //
-// Grid (G chunks, B rows); each workgroup streams one chunk of 8192 logits of
-// a row (2048 in batches of at most 8 rows) into registers once (16-byte
-// loads) and applies the history penalties from an LDS table.  The greedy and
-// top-k rows' streaming pass runs 256 threads (4 waves of 64, 32 logits per
-// thread); the latency-bound launches (the top-k finisher, and the mass rows
-// in batches of at most 64 rows) run the same code at 512 threads.  Two
-// launches run side by side (one on a side stream):
-//   main launch  greedy rows: local argmax, one 64-bit atomic max per
-//                workgroup, the last workgroup to arrive publishes the id.
-//                top-k rows (0 < k <= QS_TOPK_FAST_MAX): every workgroup
-//                writes the tokens at or above a threshold taken from its
-//                per-thread maxima, in id order, to its own region; the last
-//                workgroup gathers the regions into registers (eight tokens per
-//                thread, still in id order) and resolves top-k, top-p and the
-//                draw with register radix selects over 256-bin LDS histograms.
-//   mass launch  rows with top-k off.  Every workgroup writes the tokens
-//                within 40 octaves of its own maximum; one row barrier
-//                exchanges the row maximum and the counts.  A peaked row (few
-//                such tokens) is then resolved by one workgroup like a top-k
-//                row.  A flat row stays cooperative: exact weights, per-bin
-//                masses, a second row barrier for the global histogram and the
-//                total mass, the bracket of bins holding the top-p boundary,
-//                the bracketed tokens listed; the last workgroup to arrive
-//                resolves the boundary exactly, finds the chunk holding the
-//                draw and re-reads that chunk to locate the token in id order.
+// Grid (G chunks, rows); each workgroup streams one chunk of 8192 logits of a
+// row (2048 in batches of at most 8 rows) into registers once (16-byte loads)
+// and applies the history penalties from an LDS table.  Rows are greedy,
+// top-k (0 < k <= QS_TOPK_FAST_MAX) or mass rows (top-k off).  A batch of at
+// most 64 rows with mass rows is one streaming launch (k_sample_all, at 512
+// threads: grid rows for the mass rows first, then the batch's own rows) and
+// one finishing launch (k_finish_all, one workgroup per row), on the caller's
+// stream; small batches finish each row inside the streaming launch (its
+// last workgroup to arrive).  Larger batches run the mass rows and the other
+// rows as two launches on two streams (k_sample then k_finish, per role).
+//   greedy rows  local argmax, one 64-bit atomic max per workgroup, the last
+//                workgroup to arrive publishes the id.
+//   top-k rows   every workgroup writes the tokens at or above a threshold
+//                taken from its per-thread maxima, in id order, to its own
+//                region; the finisher gathers the regions into registers
+//                (still in id order) and resolves top-k, top-p and the draw
+//                with register radix selects over LDS histograms.
+//   mass rows    every workgroup writes the tokens within 40 octaves of its
+//                own maximum; one row barrier exchanges the row maximum and
+//                the counts.  A peaked row (few such tokens) is then resolved
+//                by one workgroup like a top-k row.  A flat row stays
+//                cooperative: exact weights, per-bin masses, a second row
+//                barrier for the global histogram and the total mass, the
+//                bracket of bins holding the top-p boundary, the bracketed
+//                tokens listed; the finisher resolves the boundary exactly,
+//                finds the chunk holding the draw and re-reads one segment of
+//                it to locate the token in id order.
 //   fallback     a single workgroup resolves the row exactly from global
 //                memory (large k, a candidate overflow, an incomplete
 //                candidate set, a bracket overflow).  Slow, rare on real logits.
