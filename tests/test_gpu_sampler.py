@@ -290,3 +290,25 @@ def test_chunk_layouts_and_sparse_last_chunks(gpu, B, V, dtype):
     _check(xx, dtype, gpu, T, P, K, rep, pres, freq, hist, u=u, probs=False, paths=paths)
     why = paths[1]
     assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
+
+
+@pytest.mark.parametrize("B,V,dtype", [(40, 8192 * 6 + 123, "bf16"), (64, 50000, "f32"), (8, 30011, "bf16"),
+                                       (6, 20000, "f32")])
+def test_more_mass_rows_than_mass_slots(gpu, B, V, dtype):
+    """Batches of at most 64 rows run in one streaming launch whose first
+    min(B, 8) grid rows take the batch's first mass rows; the other mass rows
+    are streamed from their own grid rows.  Flat, peaked and no-top-p mass
+    rows mixed with top-k and greedy rows, more mass rows than slots."""
+    rng = np.random.default_rng(B * 7919 + V)
+    x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    kinds = [(1.0, 0.9, 0), (0.05, 0.95, 0), (1.3, 1.0, 0), (0.7, 0.8, 50), (0.0, 1.0, 0), (0.9, 0.6, 0)]
+    T = np.array([kinds[r % len(kinds)][0] for r in range(B)], np.float32)
+    P = np.array([kinds[r % len(kinds)][1] for r in range(B)], np.float32)
+    K = np.array([kinds[r % len(kinds)][2] for r in range(B)], np.int32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] mass slots B={B} V={V} {dtype}", flush=True)
+    paths = []
+    _check(xx, dtype, gpu, T, P, K, u=u, paths=paths)
+    why = paths[1]
+    assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
