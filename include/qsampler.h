@@ -46,9 +46,10 @@ extern "C" {
                                    sampling row has 0 < top_k <= QS_TOPK_FAST_MAX
                                    (same kind of batch flag as use_top_p,
                                    src/compute/model_runner.py:82-83); skips the
-                                   launch that serves top-k-off rows.  If such a
-                                   row is present anyway it is still resolved
-                                   exactly, by a slower path. */
+                                   code that serves top-k-off rows (batches above
+                                   64 rows: their launch).  If such a row is
+                                   present anyway it is still resolved exactly,
+                                   by a slower path. */
 
 #define QS_TOPK_FAST_MAX 1024 /* top_k up to this value is resolved from
                                  per-chunk candidates in one pass */
