@@ -139,7 +139,9 @@ struct __attribute__((aligned(64))) Slot {
   u32 below;       // top-k rows: largest z key below tau in the chunk
   u32 nbr;         // flat mass rows: bracketed tokens of the chunk
   u32 nse;         // flat mass rows: (key, segment) entries of the chunk (0xffffffff: more than fit)
-  u32 pad[3];
+  u32 kmx;         // mass rows: the chunk's largest key of q
+  u32 nkmn;        // mass rows: ~ its smallest key of q (over tokens with a key)
+  u32 pad;
 };
 static_assert(sizeof(Slot) == 64, "slot is 64 bytes");
 
