@@ -106,8 +106,8 @@ enum : u32 {
 // leaves at zero; the rest holds the last call's result for k_probs.
 struct __attribute__((aligned(256))) RowCtl {
   u64 pack;        // greedy: max of (gkey << 32 | ~id)
-  u32 arrive;      // workgroups done
-  u32 bar;         // row barrier counter
+  u32 arrive;      // arrival lines all of whose workgroups are done (see arrive_last)
+  u32 bar_unused;  // (row barriers count in Args::bars)
   u32 kmax;        // mass rows: max key(q)
   u32 nkmin;       // mass rows: ~min key(q) over non-NaN tokens
   u32 status;      // kSt* flags
@@ -129,6 +129,7 @@ struct __attribute__((aligned(256))) RowCtl {
 };
 static_assert(sizeof(RowCtl) == 256, "row control block is 256 bytes");
 constexpr int kCtlZeroWords = 16;
+constexpr int kSubLines = 8;  // cache lines a row's barrier and arrival counters are spread over
 
 // Per-(row, workgroup) published values.
 struct __attribute__((aligned(64))) Slot {
@@ -168,6 +169,7 @@ struct Args {
   u64* sent;   // [B, G, kSegEnt] per chunk: bracket entries (key << 32 | segment << 16 | count), flat mass rows
   u64* segm;   // [B, G, kSegs, 2] flat mass rows: exact mass per segment (above the bracket with top-p), lo, hi
   Slot* slots; // [B, G]
+  u32* bars;    // [B, 2, kSubLines, 32]: row-barrier and arrival counters, one per cache line
   u64* trace;  // per-workgroup phase timestamps (trace builds only)
 };
 
@@ -452,7 +454,7 @@ constexpr int ns_threads(int ns) { return ns == kNsW512 ? 512 : 256; }
 struct Layout {
   bool small;  // kCHSmall chunks (the n2k kernels)
   int kch, G, R, logR, seg_cap, Hpad;
-  size_t off_ctl, off_cand, off_hist, off_list, off_slots, off_segm, off_sent, total;
+  size_t off_ctl, off_cand, off_hist, off_list, off_slots, off_segm, off_sent, off_bars, total;
   size_t lds_sample0, lds_sample1;  // k_sample of greedy and top-k rows, of mass rows
   int ns_sample[2], ns_finish[2];  // builds of k_sample and k_finish, per role
   size_t lds_finish[3];                   // k_finish (and a fused k_sample's tail), per build
@@ -517,6 +519,8 @@ Layout layout_for(int B, int V, int H) {
   o = align_up(o + (size_t)B * L.G * kSegs * 16, 256);
   L.off_sent = o;
   o = align_up(o + (size_t)B * L.G * kSegEnt * 8, 256);
+  L.off_bars = o;
+  o = align_up(o + (size_t)B * 2 * kSubLines * 128, 256);
   L.total = o;
   const size_t pen = H > 0 ? (size_t)L.kch * 2 : 0;  // 16-bit history counts of one chunk
   L.lds_finish[kNsW256] = finish_lds<LdsLarge>(pen, H, L.Hpad);
@@ -703,6 +707,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   a.slots = (Slot*)(base + L.off_slots);
   a.segm = (u64*)(base + L.off_segm);
   a.sent = (u64*)(base + L.off_sent);
+  a.bars = (u32*)(base + L.off_bars);
 #ifdef QS_TRACE
   a.trace = g_trace;
 #endif
