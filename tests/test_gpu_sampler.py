@@ -312,3 +312,74 @@ def test_more_mass_rows_than_mass_slots(gpu, B, V, dtype):
     _check(xx, dtype, gpu, T, P, K, u=u, paths=paths)
     why = paths[1]
     assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
+
+
+def _mixed_rows(B, V, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.gumbel(size=(B, V)) * rng.uniform(1.0, 4.0, size=(B, 1))).astype(np.float32)
+    kinds = [(1.0, 0.9, 0), (0.3, 0.8, 300), (1.3, 1.0, 0), (0.7, 0.8, 50), (0.0, 1.0, 0), (0.9, 0.6, 0),
+             (1.1, 0.95, 1000), (0.05, 0.95, 0)]
+    T = np.array([kinds[r % len(kinds)][0] for r in range(B)], np.float32)
+    P = np.array([kinds[r % len(kinds)][1] for r in range(B)], np.float32)
+    K = np.array([kinds[r % len(kinds)][2] for r in range(B)], np.int32)
+    return x, T, P, K, rng
+
+
+@pytest.mark.parametrize("B,V,dtype", [(72, W.VOCAB, "bf16"), (100, W.VOCAB, "f32")])
+def test_mixed_batches_above_64_rows(gpu, B, V, dtype):
+    """Batches above 64 rows run the mass rows and the other rows as two
+    launches on two streams (event fork and join); mixed kinds against the
+    oracle, every row on its fast path at the full vocabulary.  (At small V
+    a top-k of 1000 over bf16 ties can exceed what the per-chunk regions
+    hold; such rows are resolved exactly by the single-workgroup path.)"""
+    x, T, P, K, rng = _mixed_rows(B, V, B * 31 + V)
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] two-stream batch B={B} V={V} {dtype}", flush=True)
+    paths = []
+    _check(xx, dtype, gpu, T, P, K, u=u, paths=paths)
+    why = paths[1]
+    assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
+
+
+def test_graph_replays_two_streams(gpu):
+    """Replays of a captured two-stream call (B = 72) match the eager calls."""
+    B, V = 72, 8192 * 12 + 77
+    x, T, P, K, rng = _mixed_rows(B, V, 4242)
+    lg = _dev_logits(W.bf16_bits(x), "bf16", gpu)
+    t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to(device=gpu, dtype=dt)
+    Td, Pd, Kd = t(T, torch.float32), t(P, torch.float32), t(K, torch.int32)
+    U = [t(rng.random(B).astype(np.float32), torch.float32) for _ in range(2)]
+    ws = Workspace(B, V, torch.bfloat16, 0, gpu)
+    outs = [torch.empty(B, dtype=torch.int64, device=gpu) for _ in range(2)]
+
+    def steps():
+        for s in range(2):
+            sample_into(lg, outs[s], ws, temperatures=Td, top_ps=Pd, top_ks=Kd, uniforms=U[s], use_top_p=True,
+                        mass_rows=True)
+
+    print("[edge] graph replays, two streams", flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        steps()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    eager = [o.cpu().numpy().copy() for o in outs]
+    for s in range(2):
+        ref = contract.sample(W.bf16_bits(x), "bf16", T, P, K, None, None, None, None, U[s].cpu().numpy(),
+                              want_probs=False)
+        np.testing.assert_array_equal(eager[s], ref.ids)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        steps()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for s in range(2):
+            np.testing.assert_array_equal(outs[s].cpu().numpy(), eager[s])
+        steps()  # eager work between replays
+        torch.cuda.synchronize()
