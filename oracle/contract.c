@@ -2,7 +2,7 @@
  * CPU oracle for the decode-step sampler -- TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
- * this file's library, and only as the checker or the timed CPU baseline. The
+ * this file's library, and only to check results or as the timed CPU baseline. The
  * product path (qedge_amd/) never calls it.
  *
  * What it restates. The reference sampler is BatchSampler.forward

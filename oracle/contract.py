@@ -1,7 +1,7 @@
 """ctypes front of the CPU oracle (oracle/contract.c) -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
-may import this module, as the checker or the timed CPU baseline.  The product
+may import this module, to check results or as the timed CPU baseline.  The product
 path never does.
 
 The oracle restates src/compute/sampler.py:25-41 (with the staging rules of
