@@ -163,7 +163,7 @@ struct Args {
   float* out_probs;
   int* out_kept;
   RowCtl* ctl;
-  uint4* cand; // [B, G, R] region entries {id, q key, exp2 mantissa M, octave n}
+  u64* cand;   // [B, G, R] region entries (key of q) << 32 | id
   u64* mhist;  // [B, kWBins] flat mass rows: the row's sums of mantissas per bin
   u64* list;   // [B, kListCap] bracket entries (key << 32 | chunk << 16 | count), flat mass rows
   u64* sent;   // [B, G, kSegEnt] per chunk: bracket entries (key << 32 | segment << 16 | count), flat mass rows
@@ -508,7 +508,7 @@ Layout layout_for(int B, int V, int H) {
   L.off_ctl = o;
   o = align_up(o + (size_t)B * sizeof(RowCtl), 256);
   L.off_cand = o;
-  o = align_up(o + (size_t)B * L.G * L.R * 16, 256);
+  o = align_up(o + (size_t)B * L.G * L.R * 8, 256);
   L.off_hist = o;
   o = align_up(o + (size_t)B * kWBins * 8, 256);
   L.off_list = o;
@@ -701,7 +701,7 @@ int run(const void* logits, int64_t row_stride, int dtype, int B, int V, const f
   a.out_kept = out_kept;
   char* base = (char*)ws;
   a.ctl = (RowCtl*)(base + L.off_ctl);
-  a.cand = (uint4*)(base + L.off_cand);
+  a.cand = (u64*)(base + L.off_cand);
   a.mhist = (u64*)(base + L.off_hist);
   a.list = (u64*)(base + L.off_list);
   a.slots = (Slot*)(base + L.off_slots);
