@@ -72,6 +72,7 @@ class Case:
         self.uniforms = [t(w.uniforms(s), torch.float32) for s in range(R)]
         H = 0 if w.history is None else w.history.shape[1]
         self.ws = Workspace(B, V, base.dtype, H, device)
+        self.order = t(dispatch_order(w), torch.int32)
         self.ids = torch.empty(B, dtype=torch.int64, device=device)
         self.alg_bytes = w.algorithmic_bytes()
 
@@ -80,7 +81,22 @@ class Case:
 
         r = i % self.R
         sample_into(self.logits[r], self.ids, self.ws, uniforms=self.uniforms[r], use_top_p=True,
-                    mass_rows=self.w.mass_rows, **self.params)
+                    row_order=self.order, **self.params)
+
+
+def dispatch_order(w):
+    """The row order the host stages beside the parameters (qedge_amd.batch.SamplingBatch):
+    rows with top-k off first, then top-k rows by descending k, greedy rows last."""
+    import numpy as np
+
+    def kind(t, k):
+        if t <= 1e-5:
+            return 2
+        return 1 if 0 < k < w.V and k <= 1024 else 0
+
+    rank = sorted((kind(w.temperature[r], w.top_k[r]), 0 if w.temperature[r] <= 1e-5 else -int(w.top_k[r]), r)
+                  for r in range(w.nrows))
+    return np.array([r for _, _, r in rank], np.int32)
 
 
 def time_graph(case: Case, steps: int, warmup: int, repeats: int = 5):

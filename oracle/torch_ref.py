@@ -20,8 +20,8 @@ the kernels' sets and probabilities against the reference's own arithmetic.
 
 ``extended_forward`` adds the build's extensions in torch ops, in the order the
 kernels apply them: history penalties (repetition, then frequency, then
-presence), temperature, top-k keeping ties at the k-th value, then top-p on the
-top-k set.  It is what the CPU baseline times for workloads that use them.
+presence), temperature, top-k keeping ties at the k-th value, min_p (keep
+p >= min_p * p_max), then top-p on the remaining set.  It is what the CPU baseline times for workloads that use them.
 """
 from __future__ import annotations
 
@@ -84,9 +84,15 @@ class FilterState:
     argmax: torch.Tensor     # int64 [B] argmax of z (first index, NaN is maximum)
 
 
+def _min_p_mask(scaled: torch.Tensor, min_ps: torch.Tensor) -> torch.Tensor:
+    """Tokens with p >= min_p * p_max, evaluated as q - q_max >= log(min_p)."""
+    ratio = torch.exp(scaled - scaled.max(dim=-1, keepdim=True).values)
+    return ratio >= min_ps.unsqueeze(1)
+
+
 def filter_rows(logits: torch.Tensor, temperatures: torch.Tensor, top_ps: torch.Tensor | None = None,
                 top_ks: torch.Tensor | None = None, rep=None, pres=None, freq=None, history=None,
-                use_top_p: bool = True) -> FilterState:
+                use_top_p: bool = True, min_ps: torch.Tensor | None = None) -> FilterState:
     """The reference's filtering state (src/compute/sampler.py:30-37), with the extensions.
 
     Without penalties and top-k this is exactly the reference's arithmetic; the
@@ -108,6 +114,8 @@ def filter_rows(logits: torch.Tensor, temperatures: torch.Tensor, top_ps: torch.
         kk = torch.where(on, k, torch.full_like(k, V))
         kth = torch.sort(scaled, dim=-1, descending=True).values.gather(1, (kk - 1).clamp(min=0).unsqueeze(1))
         scaled = torch.where(on.unsqueeze(1) & (scaled < kth), torch.full_like(scaled, float("-inf")), scaled)
+    if min_ps is not None:
+        scaled = torch.where(_min_p_mask(scaled, min_ps), scaled, torch.full_like(scaled, float("-inf")))
     probs = torch.softmax(scaled, dim=-1)
     desc, order = torch.sort(probs, dim=-1, descending=True, stable=True)
     excl_sorted = desc.cumsum(dim=-1) - desc
@@ -124,8 +132,9 @@ def filter_rows(logits: torch.Tensor, temperatures: torch.Tensor, top_ps: torch.
 
 def extended_forward(logits: torch.Tensor, temperatures: torch.Tensor, top_ps: torch.Tensor | None,
                      top_ks: torch.Tensor | None = None, rep=None, pres=None, freq=None, history=None,
-                     use_top_p: bool = True, generator: torch.Generator | None = None) -> torch.Tensor:
-    """The full extended sampler in torch-CPU ops (penalties, top-k, top-p, multinomial)."""
+                     use_top_p: bool = True, generator: torch.Generator | None = None,
+                     min_ps: torch.Tensor | None = None) -> torch.Tensor:
+    """The full extended sampler in torch-CPU ops (penalties, top-k, min_p, top-p, multinomial)."""
     z = logits.float()
     B, V = z.shape
     if history is not None:
@@ -141,6 +150,8 @@ def extended_forward(logits: torch.Tensor, temperatures: torch.Tensor, top_ps: t
         kk = torch.where(on, k, torch.full_like(k, V))
         kth = desc_z.gather(1, (kk - 1).clamp(min=0).unsqueeze(1))
         desc_z = torch.where(desc_z < kth, torch.full_like(desc_z, float("-inf")), desc_z)
+    if min_ps is not None:
+        desc_z = torch.where(_min_p_mask(desc_z, min_ps), desc_z, torch.full_like(desc_z, float("-inf")))
     desc = torch.softmax(desc_z, dim=-1)
     if use_top_p and top_ps is not None:
         drop = (desc.cumsum(dim=-1) - desc) > top_ps.unsqueeze(1)

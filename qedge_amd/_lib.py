@@ -16,10 +16,12 @@ QS_DTYPE_F32 = 0
 QS_DTYPE_BF16 = 1
 QS_FLAG_ALL_GREEDY = 1
 QS_FLAG_USE_TOP_P = 2
-QS_FLAG_NO_MASS_ROWS = 4
+QS_FLAG_NO_WAIT = 4
 QS_TOPK_FAST_MAX = 1024
+QS_MAX_HISTORY = 65535
 
-EXPORTS = ("qs_version", "qs_last_error", "qs_workspace_bytes", "qs_workspace_init", "qs_sample", "qs_argmax")
+EXPORTS = ("qs_version", "qs_last_error", "qs_workspace_bytes", "qs_workspace_init", "qs_sample", "qs_argmax",
+           "qs_history_append", "qs_step_finish")
 
 _lib = None
 
@@ -45,9 +47,21 @@ def load():
     lib.qs_workspace_init.restype = I
     lib.qs_workspace_init.argtypes = [P, SZ, P]
     lib.qs_sample.restype = I
-    lib.qs_sample.argtypes = [P, I64, I, I, I, P, P, P, P, P, P, P, I, P, U32, P, P, P, P, SZ, P]
+    lib.qs_sample.argtypes = [P, I64, I, I, I,          # logits, row_stride, dtype, B, V
+                              P, P, P, P,               # temperature, top_p, top_k, min_p
+                              P, P, P,                  # rep, pres, freq
+                              P, I, P,                  # hist_ids, H, hist_len
+                              P, P, U32,                # uniforms, row_order, flags
+                              P, P, P,                  # out_ids, out_probs, out_kept
+                              P, SZ, P]                 # workspace, bytes, stream
     lib.qs_argmax.restype = I
     lib.qs_argmax.argtypes = [P, I64, I, I, I, P, P, SZ, P]
+    if hasattr(lib, "qs_history_append"):
+        lib.qs_history_append.restype = I
+        lib.qs_history_append.argtypes = [P, I, I, P, P, P, P]
+    if hasattr(lib, "qs_step_finish"):
+        lib.qs_step_finish.restype = I
+        lib.qs_step_finish.argtypes = [P, I, P, P, I, P, P, P, P, P, I, P, P]
     _lib = lib
     return lib
 

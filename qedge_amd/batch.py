@@ -56,11 +56,14 @@ class SamplingBatch:
         self.presence_penalties = torch.zeros(max_bs, **f32)
         self.frequency_penalties = torch.zeros(max_bs, **f32)
         self.uniforms = torch.zeros(max_bs, **f32)
+        self.row_order = torch.zeros(max_bs, dtype=torch.int32, device=device)
         self.max_history = max_history
         self.history = (torch.full((max_bs, max_history), -1, dtype=torch.int32, device=device)
                         if max_history > 0 else None)
         self._staging: dict[tuple[int, torch.dtype], torch.Tensor] = {}
+        self._staged: dict[tuple[int, torch.dtype], object] = {}  # event of the last copy out of each buffer
         self._signature: tuple | None = None
+        self._order_sig: tuple | None = None
         self._rng = np.random.default_rng()
         self.bs = 0
         self.all_greedy = True
@@ -73,7 +76,11 @@ class SamplingBatch:
         self.max_top_k = 0
 
     def _cp(self, dst: torch.Tensor, data, dtype: torch.dtype) -> None:
-        """Write ``data`` into reusable pinned staging, then a non-blocking H2D copy (:75-88)."""
+        """Write ``data`` into reusable pinned staging, then a non-blocking H2D copy (:75-88).
+
+        The staging buffer is rewritten only after the previous copy out of it
+        has completed (an event recorded after each copy), so a step never
+        overwrites the values of a step whose copy is still queued."""
         flat = dst.reshape(-1)
         key = (flat.data_ptr(), dtype)
         cpu = self._staging.get(key)
@@ -81,9 +88,17 @@ class SamplingBatch:
         if cpu is None or cpu.numel() < flat.numel():
             cpu = torch.empty(flat.numel(), dtype=dtype, pin_memory=pin)
             self._staging[key] = cpu
+            self._staged.pop(key, None)
+        ev = self._staged.get(key)
+        if ev is not None:
+            ev.synchronize()
         arr = np.asarray(data).reshape(-1)
         cpu.numpy()[: arr.size] = arr
         flat[: arr.size].copy_(cpu[: arr.size], non_blocking=True)
+        if pin:
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(flat.device))
+            self._staged[key] = ev
 
     def fill(self, params: list[SamplingParams], histories: list[list[int]] | None = None,
              step: int = 0) -> None:
@@ -120,8 +135,20 @@ class SamplingBatch:
         self.max_top_k = max(top_ks) if self.use_top_k else 0
         self.use_penalties = any(s.uses_penalties for s in params)
         self.mass_rows = any(not g and not (0 < k <= self.fast_topk and k < V) for g, k in zip(greedy, top_ks))
-        # history ids, padded with -1 (ignored by the sampler)
-        if histories is not None:
+        # dispatch order: rows with top-k off first (their workgroups cooperate), then
+        # top-k rows by descending k, greedy rows last; results do not depend on it
+        def kind(g: bool, k: int) -> int:
+            if g:
+                return 2
+            return 1 if 0 < k < V and k <= self.fast_topk else 0
+
+        rank = sorted((kind(g, k), 0 if g else -k, r) for r, (g, k) in enumerate(zip(greedy, top_ks)))
+        order = np.array([r for _, _, r in rank], dtype=np.int32)
+        if signature != self._order_sig:
+            self._cp(self.row_order[:bs], order, torch.int32)
+            self._order_sig = signature
+        # history ids, padded with -1 (ignored by the sampler); only when some row uses penalties
+        if histories is not None and self.use_penalties:
             if self.history is None:
                 raise ValueError("SamplingBatch was built without history buffers (max_history=0)")
             H = self.max_history
@@ -144,7 +171,9 @@ class SamplingBatch:
         bs = self.bs
         kw = dict(temperatures=self.temperatures[:bs], top_ps=self.top_ps[:bs], top_ks=self.top_ks[:bs],
                   uniforms=self.uniforms[:bs], all_greedy=self.all_greedy, use_top_p=self.use_top_p,
-                  mass_rows=self.mass_rows)
+                  row_order=self.row_order[:bs])
+        if self.use_min_p:
+            kw["min_ps"] = self.min_ps[:bs]
         if self.use_penalties:
             kw.update(repetition_penalties=self.repetition_penalties[:bs],
                       presence_penalties=self.presence_penalties[:bs],

@@ -1,0 +1,1555 @@
+// Kernels of the sampler (one launch per call).  Included by qsampler.hip.
+//
+// Grid (G, B): workgroup (c, s) streams chunk c (kCH logits) of row
+// order[s] (s itself without an order) into registers once, applies the
+// history penalties from an LDS count table, and plays its row's role:
+//   greedy  local argmax, published to the chunk's slot;
+//   top-k   the chunk's tokens at or above a threshold taken from its
+//           per-thread maxima, written in id order to the chunk's region;
+//   mass    (top-k off) keys of q in registers; one row barrier exchanges the
+//           chunk maxima (the row maximum q* anchors the weights); with top-p
+//           each workgroup publishes a 256-bin mass histogram and the last one
+//           to arrive (the reducer) picks the bin that holds the top-p
+//           boundary; then every workgroup publishes its mass above that bin
+//           and lists its tokens inside it.
+// Every workgroup then counts its arrival; the last workgroup of a row
+// resolves the row (top-k, min_p, top-p and the draw) from what the others
+// published, writes the id and returns the row's counters to zero.  Rows the
+// fast paths cannot serve exactly (top-k above kTopkMax, a region or list
+// overflow, an incomplete candidate set, a barrier time-out) are resolved by
+// that last workgroup alone with exact passes over the row.
+#pragma once
+#include "qs_device.hpp"
+#include "qsampler.h"
+
+namespace qs {
+
+constexpr int kCH = 8192;                  // logits per chunk (one workgroup)
+constexpr int kEPT = kCH / kThreads;       // logits per thread
+constexpr int kWaveSpan = kCH / kWaves;    // contiguous ids per wave
+constexpr int kMaxG = 256;                 // chunks per row
+constexpr int kRegionTotal = 8192;         // top-k candidate entries per row (G * R)
+constexpr int kTopkMax = QS_TOPK_FAST_MAX; // top-k served from candidates
+constexpr int kFPer = 16;                  // gathered entries per finishing thread
+constexpr int kFCap = kFPer * kThreads;    // gathered entries per row
+constexpr int kNB = 256;                   // mass histogram bins (one per thread)
+constexpr int kRounds = 3;                 // bracket rounds before the exact path
+constexpr int kLC = 128;                   // bracket entries per chunk
+constexpr int kNBS = 1024;                 // select histogram bins
+constexpr int kStageCap = 1024;            // entries staged in LDS by one workgroup
+
+enum : u32 { kStOverflow = 1u, kStIncomplete = 2u, kStTimeout = 4u, kStList = 8u };
+enum : u32 { kKindGreedy = 0, kKindTopK = 1, kKindMass = 2, kKindSingle = 3 };
+// How the last call resolved a row (RowRes::path).
+enum : u32 { kPathGreedy = 1, kPathTopK = 2, kPathMassTopP = 3, kPathMassAll = 4, kPathSingle = 5 };
+
+// Per-row counters, each on its own 128-byte line.  Zero between calls.
+struct __attribute__((aligned(128))) RowSync {
+  u32 arrive;  u32 p0[31];
+  u32 status;  u32 p1[31];
+  u32 barA;    u32 p2[31];
+  u32 barB;    u32 p3[31];
+  u32 dec;     u32 p4[31];
+};
+// Per-row result of the last call (read by k_probs and by the tests).
+struct __attribute__((aligned(128))) RowRes {
+  long long id;
+  u64 W, thr;       // kept mass, min_p threshold on weights
+  u64 Tp, S, Ahi;   // mass rows with top-p: floor(top_p * S), S, mass above the boundary bin
+  u32 kind, path, why;
+  u32 kstar;        // key of q*
+  u32 klo, idlo;    // kept iff key > klo || (key == klo && id <= idlo), and weight > 0
+  u32 kept;
+  u32 pad[13];
+};
+static_assert(sizeof(RowRes) == 128, "row result is 128 bytes");
+// Per-(row, chunk) published values.
+struct __attribute__((aligned(32))) Slot {
+  u64 a;  // greedy: (gkey << 32 | ~id); top-k: (below << 32 | n); mass: (kmax << 32 | kmin)
+  u64 b;  // mass: S_c (total weight), then mass above the boundary bin
+  u64 c;  // mass: count of nonzero weights; then (n listed << 32 | count above)
+  u64 d;
+};
+
+struct Args {
+  const void* logits;
+  long long row_stride;
+  int B, V, G, R, SH, H;
+  int vec_ok;
+  u32 flags, spin_limit;
+  const float* temperature;
+  const float* top_p;
+  const int* top_k;
+  const float* min_p;
+  const float* rep;
+  const float* pres;
+  const float* freq;
+  const int* hist;       // [B, H]
+  const int* hist_len;   // [B] or null: row r uses hist[r, 0:hist_len[r]]
+  const float* uniforms;
+  const int* order;      // [B] or null
+  long long* out_ids;
+  float* out_probs;
+  int* out_kept;
+  RowSync* sync;
+  RowRes* res;
+  Slot* slots;  // [B, kMaxG]
+  u64* data;    // [B, data_per_row]
+  long long data_per_row;  // u64 entries
+};
+
+struct RowP {
+  float T, rT, tp, mp, rep, pres, freq, u;
+  int k, kind, hlen;
+  bool t_one, topp, pen;
+  const int* hist;
+};
+
+__device__ __forceinline__ RowP row_params(const Args& a, int row) {
+  RowP p;
+  p.T = a.temperature ? a.temperature[row] : 0.0f;
+  const bool greedy = (a.flags & QS_FLAG_ALL_GREEDY) || (p.T <= 1e-5f);
+  p.k = a.top_k ? a.top_k[row] : 0;
+  const bool topk_on = p.k > 0 && p.k < a.V;
+  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? a.top_p[row] : 1.0f;
+  p.topp = p.tp < 1.0f;
+  p.mp = a.min_p ? a.min_p[row] : 0.0f;
+  p.rep = a.rep ? a.rep[row] : 1.0f;
+  p.pres = a.pres ? a.pres[row] : 0.0f;
+  p.freq = a.freq ? a.freq[row] : 0.0f;
+  p.hlen = a.hist ? (a.hist_len ? a.hist_len[row] : a.H) : 0;
+  if (p.hlen > a.H) p.hlen = a.H;
+  p.hist = a.hist ? a.hist + (size_t)row * a.H : nullptr;
+  p.pen = p.hist != nullptr && p.hlen > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
+  p.u = a.uniforms ? a.uniforms[row] : 0.0f;
+  if (!(p.u >= 0.0f)) p.u = 0.0f;
+  if (p.u >= 1.0f) p.u = __uint_as_float(0x3f7fffffu);
+  p.kind = greedy ? kKindGreedy : (topk_on ? (p.k <= kTopkMax ? kKindTopK : kKindSingle) : kKindMass);
+  p.t_one = p.T == 1.0f;
+  p.rT = 1.0f / p.T;
+  return p;
+}
+
+// ---------------------------------------------------------------- LDS
+
+struct SelLds {
+  u32 hc[kNBS];
+  u64 hm[kNBS];
+};
+struct Lds {
+  union {
+    u32 pen[kCH / 2];       // history counts of the chunk, two 16-bit counts per word
+    u64 mh[kNB];            // mass histogram of the chunk
+    u64 stage[kStageCap];   // entries staged for a region
+  } u;
+  SelLds sel;               // select histogram (beside the table: the exact pass needs both)
+  u32 hc[kNB];              // counts of the mass histogram
+  u64 cmass[kMaxG];         // finisher: per-chunk masses
+  u32 cties[kMaxG];         // finisher: per-chunk tie counts
+  u32 coff[kMaxG + 1];      // finisher: gathered offsets per chunk
+  Scratch s;
+};
+
+// ---------------------------------------------------------------- chunk in registers
+
+template <int DT>
+struct Chunk {
+  static constexpr int VL = DT == QS_DTYPE_F32 ? 4 : 8;  // logits per 16-byte vector
+  static constexpr int J = kEPT / VL;                    // vectors per thread
+  uint4 v[J];
+  int nval;  // valid logits of this thread's span: element (j, e) is valid iff j*64*VL + e < nval
+  int base;  // id of element (0, 0)
+  __device__ __forceinline__ int id(int j, int e) const { return base + j * 64 * VL + e; }
+  __device__ __forceinline__ bool valid(int j, int e) const { return j * 64 * VL + e < nval; }
+  __device__ __forceinline__ float raw(int j, int e) const {
+    const uint4 q = v[j];
+    if (DT == QS_DTYPE_F32) {
+      const u32 w = e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w;
+      return __uint_as_float(w);
+    }
+    const u32 w = (e >> 1) == 0 ? q.x : (e >> 1) == 1 ? q.y : (e >> 1) == 2 ? q.z : q.w;
+    return bf16_to_f32((e & 1) ? (w >> 16) : (w & 0xffffu));
+  }
+};
+
+// Issue the loads of chunk c of a row (no wait).
+template <int DT>
+__device__ __forceinline__ void load_chunk(const Args& a, int row, int c, Chunk<DT>& ch) {
+  constexpr int VL = Chunk<DT>::VL;
+  const int l = lane_id(), w = wave_id();
+  ch.base = c * kCH + w * kWaveSpan + l * VL;
+  ch.nval = a.V - ch.base;
+  const size_t rowoff = (size_t)row * (size_t)a.row_stride;
+#pragma unroll
+  for (int j = 0; j < Chunk<DT>::J; ++j) {
+    const int i0 = ch.base + j * 64 * VL;
+    if (a.vec_ok && i0 + VL <= a.V) {
+      if (DT == QS_DTYPE_F32)
+        ch.v[j] = *(const uint4*)((const float*)a.logits + rowoff + i0);
+      else
+        ch.v[j] = *(const uint4*)((const uint16_t*)a.logits + rowoff + i0);
+    } else {
+      u32 x[4] = {0u, 0u, 0u, 0u};
+      if (DT == QS_DTYPE_F32) {
+        const float* p = (const float*)a.logits + rowoff;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i0 + e < a.V) x[e] = __float_as_uint(p[i0 + e]);
+      } else {
+        const uint16_t* p = (const uint16_t*)a.logits + rowoff;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (i0 + e < a.V) x[e >> 1] |= (u32)p[i0 + e] << ((e & 1) * 16);
+      }
+      ch.v[j] = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+  }
+}
+
+// History counts of the ids in [c*kCH, (c+1)*kCH) into the LDS table.
+__device__ __forceinline__ void pen_build(const RowP& p, int c, Lds& L) {
+  uint4* t4 = (uint4*)L.u.pen;
+  for (int i = threadIdx.x; i < kCH / 8; i += kThreads) t4[i] = make_uint4(0u, 0u, 0u, 0u);
+  lds_sync();
+  const int lo = c * kCH;
+  for (int i = threadIdx.x; i < p.hlen; i += kThreads) {
+    const int d = p.hist[i] - lo;
+    if ((unsigned)d < (unsigned)kCH) atomicAdd(&L.u.pen[d >> 1], (d & 1) ? 0x10000u : 1u);
+  }
+  lds_sync();
+}
+// Count of element (j, e) of the thread from the table.
+template <int DT>
+__device__ __forceinline__ u32 pen_count(const Lds& L, const Chunk<DT>& ch, int c, int j, int e) {
+  const int li = ch.base - c * kCH + j * 64 * Chunk<DT>::VL + e;
+  return (L.u.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
+}
+// z of element (j, e): the logit with the penalties applied.
+template <int DT>
+__device__ __forceinline__ float elem_z(const Chunk<DT>& ch, const RowP& p, const Lds& L, int c, int j, int e) {
+  float z = ch.raw(j, e);
+  if (p.pen) {
+    const u32 n = pen_count(L, ch, c, j, e);
+    if (n) z = apply_penalty(z, n, p.rep, p.pres, p.freq);
+  }
+  return z;
+}
+// Keys of q = z / T for every element (0 for NaN and invalid elements).
+template <int DT>
+__device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, const Lds& L, int c, u32 (&kq)[kEPT]) {
+#pragma unroll
+  for (int j = 0; j < Chunk<DT>::J; ++j)
+#pragma unroll
+    for (int e = 0; e < Chunk<DT>::VL; ++e) {
+      const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+      kq[j * Chunk<DT>::VL + e] = ch.valid(j, e) ? skey(q) : 0u;
+    }
+}
+
+// ---------------------------------------------------------------- row synchronisation
+
+// Count this workgroup in *ctr after its stores completed; returns the count
+// before it (to every thread).
+__device__ __forceinline__ u32 arrive(u32* ctr, Scratch& s) {
+  wait_mem();
+  lds_sync();
+  if (threadIdx.x == 0) s.r[0] = addc(ctr, 1u);
+  lds_sync();
+  return s.r[0];
+}
+// Thread 0 waits until *ctr >= target (or the row failed / the limit passed).
+// Returns true when the target was reached, to every thread.
+__device__ __forceinline__ bool wait_count(const Args& a, int row, const u32* ctr, u32 target, Scratch& s) {
+  if (threadIdx.x == 0) {
+    bool ok = false;
+    for (u32 it = 0;; ++it) {
+      const u32 v = ldc(ctr), st = ldc(&a.sync[row].status);
+      if (v >= target) {
+        ok = true;
+        break;
+      }
+      if (st != 0u) break;
+      if (it >= a.spin_limit) {
+        orc(&a.sync[row].status, kStTimeout);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    s.r[1] = ok ? 1u : 0u;
+  }
+  lds_sync();
+  return s.r[1] != 0u;
+}
+__device__ __forceinline__ void fail_row(const Args& a, int row, u32 why) {
+  if (threadIdx.x == 0) orc(&a.sync[row].status, why);
+}
+// The last workgroup of a row returns the row's counters to zero.
+__device__ __forceinline__ void reset_row(const Args& a, int row) {
+  if (threadIdx.x == 0) {
+    RowSync* y = &a.sync[row];
+    stc(&y->arrive, 0u);
+    stc(&y->status, 0u);
+    stc(&y->barA, 0u);
+    stc(&y->barB, 0u);
+    stc(&y->dec, 0u);
+  }
+}
+__device__ __forceinline__ u64* row_data(const Args& a, int row) { return a.data + (size_t)row * a.data_per_row; }
+__device__ __forceinline__ Slot* row_slots(const Args& a, int row) { return a.slots + (size_t)row * kMaxG; }
+
+__device__ __forceinline__ void write_result(const Args& a, int row, const RowP& p, long long id, u64 W, u64 thr,
+                                             u32 path, u32 why, u32 kstar, u32 klo, u32 idlo, u32 kept) {
+  if (threadIdx.x == 0) {
+    a.out_ids[row] = id;
+    if (a.out_kept) a.out_kept[row] = (int)kept;
+    RowRes* r = &a.res[row];
+    r->id = id;
+    r->W = W;
+    r->thr = thr;
+    r->kind = (u32)p.kind;
+    r->path = path;
+    r->why = why;
+    r->kstar = kstar;
+    r->klo = klo;
+    r->idlo = idlo;
+    r->kept = kept;
+  }
+}
+
+// ---------------------------------------------------------------- selection over a set of (key, weight)
+//
+// Finds, among items with key in a range, the key kappa at which a running
+// total (counts, or weights) taken in key-descending order crosses a target:
+// total(key > kappa) <= target < total(key >= kappa) for weights, and
+// count(key > kappa) < target <= count(key >= kappa) for counts.  Each round
+// histograms the range into kNBS bins of 2^s keys (s chosen so the range
+// fits), finds the crossing bin and narrows to it; the last round has bins of
+// one key.  Items are fed by the caller through add(); rounds() drives it.
+struct Sel {
+  u32 hi, lo;   // current key range [lo, hi]
+  int s;        // bin width 2^s
+  bool by_mass;
+  u64 target;   // remaining target inside the range
+  u64 above_m;  // weight above the range (accumulated)
+  u32 above_c;  // count above the range
+  u32 found;    // 1 when kappa is found
+  u32 kappa, kcount;  // result and its multiplicity
+  u64 kmass;          // weight of the items at kappa
+};
+__device__ __forceinline__ void sel_init(Sel& q, u32 lo, u32 hi, bool by_mass, u64 target) {
+  q.lo = lo;
+  q.hi = hi;
+  const u32 width = hi - lo;  // + 1 keys
+  const int bits = bitlen(width);
+  q.s = bits > 10 ? bits - 10 : 0;
+  q.by_mass = by_mass;
+  q.target = target;
+  q.above_m = 0;
+  q.above_c = 0;
+  q.found = 0;
+  q.kappa = 0;
+  q.kcount = 0;
+  q.kmass = 0;
+}
+__device__ __forceinline__ void sel_clear(Lds& L) {
+  for (int i = threadIdx.x; i < kNBS; i += kThreads) {
+    L.sel.hc[i] = 0u;
+    L.sel.hm[i] = 0ull;
+  }
+}
+__device__ __forceinline__ void sel_add(const Sel& q, Lds& L, u32 key, u64 w) {
+  if (key >= q.lo && key <= q.hi) {
+    const u32 b = (q.hi - key) >> q.s;
+    atomicAdd(&L.sel.hc[b], 1u);
+    if (w) atomicAdd(&L.sel.hm[b], w);
+  }
+}
+// After the items of a round were added (and lds_sync'd): find the crossing
+// bin, narrow the range.  Returns true when kappa is found.
+__device__ __forceinline__ bool sel_step(Sel& q, Lds& L) {
+  constexpr int P = kNBS / kThreads;
+  const int b0 = threadIdx.x * P;
+  u32 c = 0;
+  u64 m = 0;
+  u32 hc[P];
+  u64 hm[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    hc[i] = L.sel.hc[b0 + i];
+    hm[i] = L.sel.hm[b0 + i];
+    c += hc[i];
+    m += hm[i];
+  }
+  u32 ctot;
+  u64 mtot;
+  block_excl2(c, m, L.s, &ctot, &mtot);
+  // crossing bin: the first (in key-descending order) whose inclusive total passes the target
+  if (threadIdx.x == 0) L.s.r[4] = 0xffffffffu;
+  lds_sync();
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const bool hit = q.by_mass ? (m <= q.target && q.target < m + hm[i]) : (c < q.target && q.target <= c + hc[i]);
+    if (hit) {
+      L.s.r[4] = (u32)(b0 + i);
+      L.s.r64[4] = m;
+      L.s.r[5] = c;
+      L.s.r[6] = hc[i];
+      L.s.r64[5] = hm[i];
+    }
+    c += hc[i];
+    m += hm[i];
+  }
+  lds_sync();
+  const u32 b = L.s.r[4];
+  if (b == 0xffffffffu) {  // no crossing: the target is beyond the range's total
+    q.found = 2;
+    lds_sync();
+    return true;
+  }
+  const u64 mb = L.s.r64[4], hmb = L.s.r64[5];
+  const u32 cb = L.s.r[5], hcb = L.s.r[6];
+  lds_sync();
+  q.above_m += mb;
+  q.above_c += cb;
+  if (q.by_mass)
+    q.target -= mb;
+  else
+    q.target -= cb;
+  const u32 nhi = q.hi - (b << q.s);
+  const u32 span = (1u << q.s) - 1u;
+  const u32 nlo = (nhi - q.lo) > span ? nhi - span : q.lo;
+  if (q.s == 0) {
+    q.found = 1;
+    q.kappa = nhi;
+    q.kcount = hcb;
+    q.kmass = hmb;
+    return true;
+  }
+  q.hi = nhi;
+  q.lo = nlo;
+  q.s = q.s > 10 ? q.s - 10 : 0;
+  return false;
+}
+
+// ---------------------------------------------------------------- id-order walk of a chunk in registers
+//
+// For the chunk held as Chunk<DT> by the workgroup, kw(i) gives element i's
+// kept weight (0 if not kept outright) and whether it is a tie at the
+// boundary key.  With ties counting wt each up to jties of them, finds the
+// element at which the inclusive id-order total crosses t and returns its id
+// (or -1).  Id order is (wave, j, lane, e).
+struct KW {
+  u64 w;
+  bool tie;
+};
+template <int DT, typename F>
+__device__ __forceinline__ int chunk_locate(const Chunk<DT>& ch, F&& kw, u64 wt, u32 jties, u64 t, Lds& L) {
+  constexpr int VL = Chunk<DT>::VL, J = Chunk<DT>::J;
+  u64 ex_m[J];
+  u32 ex_t[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    u64 m = 0;
+    u32 tc = 0;
+#pragma unroll
+    for (int e = 0; e < VL; ++e) {
+      const KW x = kw(j * VL + e);
+      m += x.w;
+      tc += x.tie ? 1u : 0u;
+    }
+    const u64 im = wave_incl_scan64(m);
+    const u32 it = wave_incl_scan(tc);
+    ex_m[j] = im - m;
+    ex_t[j] = it - tc;
+    if (lane_id() == 63) {
+      L.cmass[wave_id() * J + j] = im;
+      L.cties[wave_id() * J + j] = it;
+    }
+  }
+  if (threadIdx.x == 0) L.s.r[8] = 0xffffffffu;
+  lds_sync();
+  u64 off_m = 0;
+  u32 off_t = 0;
+  for (int q = 0; q < wave_id() * J; ++q) {
+    off_m += L.cmass[q];
+    off_t += L.cties[q];
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    u64 mb = off_m + ex_m[j];
+    u32 tb = off_t + ex_t[j];
+#pragma unroll
+    for (int e = 0; e < VL; ++e) {
+      const KW x = kw(j * VL + e);
+      const u64 before = mb + (u64)min(tb, jties) * wt;
+      mb += x.w;
+      tb += x.tie ? 1u : 0u;
+      const u64 after = mb + (u64)min(tb, jties) * wt;
+      if (before <= t && t < after) L.s.r[8] = (u32)ch.id(j, e);
+    }
+    off_m += L.cmass[wave_id() * J + j];
+    off_t += L.cties[wave_id() * J + j];
+  }
+  lds_sync();
+  const u32 r = L.s.r[8];
+  lds_sync();
+  return r == 0xffffffffu ? -1 : (int)r;
+}
+
+// ---------------------------------------------------------------- exact single-workgroup resolution
+//
+// Passes over the whole row from global memory, one 16-byte vector per thread
+// at a time: q* and the key range; the top-k boundary (count select, one pass
+// per round); the mass S of K; the top-p boundary (mass select); the draw and
+// the last kept tie.  Serves every row the fast paths leave (top-k above
+// kTopkMax, overflows, time-outs, rows without weights).
+
+// Calls f(m, e, z, id) for the valid elements of vector m of chunk c: thread t
+// holds vector t + m * kThreads of the chunk (VL logits).
+template <int DT, typename F>
+__device__ __forceinline__ void chunk_vec(const Args& a, const RowP& p, int row, int c, int m, const Lds& L, F&& f) {
+  constexpr int VL = DT == QS_DTYPE_F32 ? 4 : 8;
+  const int i0 = c * kCH + (m * kThreads + (int)threadIdx.x) * VL;
+  const size_t rowoff = (size_t)row * (size_t)a.row_stride;
+  u32 x[4] = {0u, 0u, 0u, 0u};
+  if (a.vec_ok && i0 + VL <= a.V) {
+    const uint4 v = DT == QS_DTYPE_F32 ? *(const uint4*)((const float*)a.logits + rowoff + i0)
+                                       : *(const uint4*)((const uint16_t*)a.logits + rowoff + i0);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  } else if (DT == QS_DTYPE_F32) {
+    const float* q = (const float*)a.logits + rowoff;
+    for (int e = 0; e < 4; ++e)
+      if (i0 + e < a.V) x[e] = __float_as_uint(q[i0 + e]);
+  } else {
+    const uint16_t* q = (const uint16_t*)a.logits + rowoff;
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < a.V) x[e >> 1] |= (u32)q[i0 + e] << ((e & 1) * 16);
+  }
+#pragma unroll
+  for (int e = 0; e < VL; ++e) {
+    if (i0 + e >= a.V) break;
+    float z = DT == QS_DTYPE_F32 ? __uint_as_float(x[e]) : bf16_to_f32((x[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+    if (p.pen) {
+      const int li = i0 + e - c * kCH;
+      const u32 n = (L.u.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
+      if (n) z = apply_penalty(z, n, p.rep, p.pres, p.freq);
+    }
+    f(m, e, z, i0 + e);
+  }
+}
+constexpr int vecs_per_chunk(int DT) { return kCH / (DT == QS_DTYPE_F32 ? 4 : 8) / kThreads; }
+
+// f(z, id) over the whole row (chunk by chunk, penalty table per chunk).
+template <int DT, typename F>
+__device__ __forceinline__ void row_pass(const Args& a, const RowP& p, int row, Lds& L, F&& f) {
+  for (int c = 0; c < a.G; ++c) {
+    if (p.pen) pen_build(p, c, L);
+    for (int m = 0; m < vecs_per_chunk(DT); ++m)
+      chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int id) { f(z, id); });
+    if (p.pen) lds_sync();
+  }
+}
+
+template <int DT>
+__device__ __noinline__ void resolve_single(const Args& a, const RowP& p, int row, u32 why, Lds& L) {
+  const int SH = a.SH;
+  const u64 thr = ceil_scaled(p.mp, 23 + SH);
+  // pass 1: key range of q over non-NaN tokens, and the greedy id for rows without weights
+  u32 kmax = 0, kmin = 0xffffffffu;
+  u64 gbest = 0;
+  row_pass<DT>(a, p, row, L, [&](float z, int id) {
+    const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));
+    kmax = max(kmax, k);
+    if (k) kmin = min(kmin, k);
+    const u64 pk = ((u64)gkey(z) << 32) | (0xffffffffu - (u32)id);
+    gbest = pk > gbest ? pk : gbest;
+  });
+  kmax = block_max(kmax, L.s);
+  kmin = ~block_max(~kmin, L.s);
+  gbest = block_max64(gbest, L.s);
+  if (kmax == 0u) {  // every q is NaN: the greedy id
+    write_result(a, row, p, (long long)(0xffffffffu - (u32)gbest), 0, thr, kPathSingle, why, 0u, 0u, 0u, 0u);
+    return;
+  }
+  const float qs = f_of_key(kmax);
+  auto key_w = [&](float z, u32& k) -> u64 {
+    const float q = qdiv(z, p.T, p.rT, p.t_one);
+    k = skey(q);
+    const u64 w = weight_of(q, k, qs, kmax, SH);
+    return w >= thr ? w : 0ull;
+  };
+  // top-k boundary: the k-th largest key (ties kept); 1 when K is every non-NaN token
+  u32 kk = 1u;
+  if (p.k > 0 && p.k < a.V) {
+    Sel q;
+    sel_init(q, kmin, kmax, false, (u64)p.k);
+    for (;;) {
+      sel_clear(L);
+      lds_sync();
+      row_pass<DT>(a, p, row, L, [&](float z, int) { sel_add(q, L, skey(qdiv(z, p.T, p.rT, p.t_one)), 0); });
+      lds_sync();
+      if (sel_step(q, L)) break;
+    }
+    if (q.found == 1) kk = q.kappa;
+  }
+  // S over K and the count of nonzero weights
+  u64 S = 0;
+  u32 nz = 0;
+  row_pass<DT>(a, p, row, L, [&](float z, int) {
+    u32 k;
+    const u64 w = key_w(z, k);
+    if (k >= kk) {
+      S += w;
+      nz += w ? 1u : 0u;
+    }
+  });
+  S = block_sum64(S, L.s);
+  nz = block_sum(nz, L.s);
+  // top-p boundary: kept iff key > klo, or key == klo among the first jties ties
+  u32 klo = kk, jties = 0xffffffffu, kept = nz;
+  u64 W = S, wt = 0;
+  if (p.topp) {
+    const u64 Tp = mul_frac(S, p.tp);
+    Sel q;
+    sel_init(q, kk, kmax, true, Tp);
+    for (;;) {
+      sel_clear(L);
+      lds_sync();
+      row_pass<DT>(a, p, row, L, [&](float z, int) {
+        u32 k;
+        const u64 w = key_w(z, k);
+        if (w && k >= kk) sel_add(q, L, k, w);
+      });
+      lds_sync();
+      if (sel_step(q, L)) break;
+    }
+    if (q.found == 1) {
+      klo = q.kappa;
+      wt = q.kmass / q.kcount;
+      const u64 A = q.above_m;
+      const u64 jj = (Tp - A) / wt + 1ull;
+      jties = (u32)(jj < (u64)q.kcount ? jj : (u64)q.kcount);
+      W = A + (u64)jties * wt;
+      kept = q.above_c + jties;
+    }
+  }
+  const bool ties_on = jties != 0xffffffffu;
+  // the draw, chunk by chunk in id order; the id of the last kept tie
+  const u64 t = mul_frac(W, p.u);
+  u64 acc = 0;         // kept mass of the chunks before, ties included
+  u64 acc_above = 0;   // the same without the ties (they count through ties_before)
+  u32 ties_before = 0;
+  int pick = -1, idlo = -1;
+  for (int c = 0; c < a.G && (pick < 0 || (ties_on && idlo < 0)); ++c) {
+    if (p.pen) pen_build(p, c, L);
+    // kept mass and ties of the chunk
+    u64 cm = 0;
+    u32 ct = 0;
+    for (int m = 0; m < vecs_per_chunk(DT); ++m)
+      chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int) {
+        u32 k;
+        const u64 w = key_w(z, k);
+        if (k >= kk && (ties_on ? k > klo : k >= klo)) cm += w;
+        if (ties_on && w && k == klo) ++ct;
+      });
+    cm = block_sum64(cm, L.s);
+    ct = block_sum(ct, L.s);
+    const u32 jl = ties_on ? (jties > ties_before ? jties - ties_before : 0u) : 0u;
+    const u64 kc = cm + (u64)min(ct, jl) * wt;
+    const bool has_pick = pick < 0 && t < acc + kc;
+    const bool has_tie = ties_on && idlo < 0 && jties > ties_before && jties <= ties_before + ct;
+    if (has_pick || has_tie) {
+      // id-order walk of the chunk: vector m of every thread, then m + 1
+      u64 run_m = acc_above;
+      u32 run_t = ties_before;
+      for (int m = 0; m < vecs_per_chunk(DT); ++m) {
+        u64 vm = 0;
+        u32 vt = 0;
+        chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int) {
+          u32 k;
+          const u64 w = key_w(z, k);
+          if (k >= kk && (ties_on ? k > klo : k >= klo)) vm += w;
+          if (ties_on && w && k == klo) ++vt;
+        });
+        u32 ttot;
+        u64 mtot;
+        u32 tex = vt;
+        u64 mex = vm;
+        block_excl2(tex, mex, L.s, &ttot, &mtot);
+        if (threadIdx.x == 0) {
+          L.s.r[8] = 0xffffffffu;
+          L.s.r[9] = 0xffffffffu;
+        }
+        lds_sync();
+        u64 mb = run_m + mex;
+        u32 tb = run_t + tex;
+        chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int id) {
+          u32 k;
+          const u64 w = key_w(z, k);
+          const bool above = k >= kk && (ties_on ? k > klo : k >= klo);
+          const bool tie = ties_on && w && k == klo;
+          const u64 before = mb + (u64)min(tb, ties_on ? jties : 0u) * wt;
+          mb += above ? w : 0ull;
+          tb += tie ? 1u : 0u;
+          const u64 after = mb + (u64)min(tb, ties_on ? jties : 0u) * wt;
+          if (before <= t && t < after) L.s.r[8] = (u32)id;
+          if (tie && tb == jties) L.s.r[9] = (u32)id;
+        });
+        lds_sync();
+        if (pick < 0 && L.s.r[8] != 0xffffffffu) pick = (int)L.s.r[8];
+        if (ties_on && idlo < 0 && L.s.r[9] != 0xffffffffu) idlo = (int)L.s.r[9];
+        lds_sync();
+        run_m += mtot;
+        run_t += ttot;
+      }
+    }
+    if (p.pen) lds_sync();
+    acc += kc;
+    acc_above += cm;
+    ties_before += ct;
+  }
+  const u32 idlo_u = ties_on ? (u32)idlo : (u32)a.V;
+  write_result(a, row, p, pick, W, thr, kPathSingle, why, kmax, klo, idlo_u, kept);
+}
+
+// ---------------------------------------------------------------- finishers
+
+// Greedy: the largest (gkey, -id) over the chunks' slots.
+__device__ __forceinline__ void finish_greedy(const Args& a, const RowP& p, int row, Lds& L) {
+  const Slot* sl = row_slots(a, row);
+  u64 best = 0;
+  for (int c = threadIdx.x; c < a.G; c += kThreads) {
+    const u64 v = ldc(&sl[c].a);
+    best = v > best ? v : best;
+  }
+  best = block_max64(best, L.s);
+  const u32 id = 0xffffffffu - (u32)best;
+  write_result(a, row, p, (long long)id, 0, 0, kPathGreedy, 0u, 0u, 0u, id, 1u);
+}
+
+// Gather the entries of per-chunk lists (counts n_c, entries at base + c*stride)
+// in chunk order into registers: thread t holds positions [t*kFPer, (t+1)*kFPer).
+// Returns the total (or 0xffffffff when it exceeds kFCap).
+__device__ __forceinline__ u32 gather_lists(const Args& a, const u64* base, int stride, const u32* counts_lds,
+                                            u64 (&ent)[kFPer], Lds& L) {
+  // offsets
+  if (threadIdx.x < 64) {
+    u32 run = 0;
+    for (int c0 = 0; c0 < a.G; c0 += 64) {
+      const int c = c0 + (int)lane_id();
+      const u32 n = c < a.G ? counts_lds[c] : 0u;
+      const u32 inc = wave_incl_scan(n);
+      if (c < a.G) L.coff[c] = run + inc - n;
+      run += readlane(inc, 63);
+    }
+    if (lane_id() == 0) L.coff[a.G] = run;
+  }
+  lds_sync();
+  const u32 total = L.coff[a.G];
+  if (total > (u32)kFCap) return 0xffffffffu;
+  // thread t: positions f = t*kFPer + i; chunk of the first by binary search
+  const u32 f0 = threadIdx.x * kFPer;
+  int c = 0;
+  {
+    int lo = 0, hi = a.G - 1;  // last c with coff[c] <= f0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (L.coff[mid] <= f0) lo = mid; else hi = mid - 1;
+    }
+    c = lo;
+  }
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) {
+    const u32 f = f0 + i;
+    while (c < a.G - 1 && L.coff[c + 1] <= f) ++c;
+    ent[i] = f < total ? ldc(base + (size_t)c * stride + (f - L.coff[c])) : 0ull;
+  }
+  return total;
+}
+
+// Finish from gathered entries (key << 32 | id) in id order, thread-contiguous:
+// select kappa_k (count k) when kk_on, weights, min_p, S, kappa_p (when top-p),
+// ties, the draw.  Returns false when the row must go to resolve_single.
+// For mass rows with top-p the entries are the boundary bin's tokens, A0 the
+// mass above it and Tp the row's target; per-chunk masses above the bin come in
+// L.cmass (already loaded) and the draw target is located to a chunk.
+__device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int row, Lds& L, u64 (&ent)[kFPer], u32 n,
+                                            u32 below_max) {
+  const int SH = a.SH;
+  const u64 thr = ceil_scaled(p.mp, 23 + SH);
+  // key range of the candidates
+  u32 kmax = 0, kmin = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) {
+    const u32 key = (u32)(ent[i] >> 32);
+    if (threadIdx.x * kFPer + i < n) {
+      kmax = max(kmax, key);
+      kmin = min(kmin, key);
+    }
+  }
+  kmax = block_max(kmax, L.s);
+  kmin = ~block_max(~kmin, L.s);
+  if (n == 0 || kmax == 0u) return false;
+  // kappa_k
+  u32 kk;
+  if (n < (u32)p.k) {
+    if (below_max != 0u) return false;  // tokens left out could belong to K
+    kk = 1u;
+  } else {
+    Sel q;
+    sel_init(q, kmin, kmax, false, (u64)p.k);
+    for (;;) {
+      sel_clear(L);
+      lds_sync();
+#pragma unroll
+      for (int i = 0; i < kFPer; ++i)
+        if (threadIdx.x * kFPer + i < n) sel_add(q, L, (u32)(ent[i] >> 32), 0);
+      lds_sync();
+      if (sel_step(q, L)) break;
+    }
+    if (q.found != 1) return false;
+    kk = q.kappa;
+    // completeness: every token left out has a key of q below kappa_k
+    if (below_max != 0u) {
+      const float zb = f_of_key(below_max);
+      const u32 kb = skey(qdiv(zb, p.T, p.rT, p.t_one));
+      if (kb >= kk) return false;
+    }
+  }
+  const float qs = f_of_key(kmax);
+  u32 wq[kFPer];  // packed weights
+  u64 S = 0;
+  u32 nz = 0;
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) {
+    const u32 key = (u32)(ent[i] >> 32);
+    u32 x = (threadIdx.x * kFPer + i < n && key >= kk) ? wpack_of(f_of_key(key), key, qs, kmax, SH) : 0u;
+    const u64 wx = wunpack(x);
+    x = wx >= thr ? x : 0u;
+    wq[i] = x;
+    S += x ? wx : 0ull;
+    nz += x ? 1u : 0u;
+  }
+  S = block_sum64(S, L.s);
+  nz = block_sum(nz, L.s);
+  u32 klo = kk, jties = 0xffffffffu, kept = nz;
+  u64 W = S, wt = 0;
+  if (p.topp) {
+    const u64 Tp = mul_frac(S, p.tp);
+    Sel q;
+    sel_init(q, kk, kmax, true, Tp);
+    for (;;) {
+      sel_clear(L);
+      lds_sync();
+#pragma unroll
+      for (int i = 0; i < kFPer; ++i)
+        if (wq[i]) sel_add(q, L, (u32)(ent[i] >> 32), wunpack(wq[i]));
+      lds_sync();
+      if (sel_step(q, L)) break;
+    }
+    if (q.found != 1) return false;
+    klo = q.kappa;
+    wt = q.kmass / q.kcount;
+    const u64 A = q.above_m;
+    const u64 jj = (Tp - A) / wt + 1ull;
+    jties = (u32)(jj < (u64)q.kcount ? jj : (u64)q.kcount);
+    W = A + (u64)jties * wt;
+    kept = q.above_c + jties;
+  }
+  // the draw over the entries in id order (thread-contiguous)
+  const u64 t = mul_frac(W, p.u);
+  u64 m = 0;
+  u32 tc = 0;
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) {
+    const u32 key = (u32)(ent[i] >> 32);
+    const bool above = jties == 0xffffffffu ? (key >= klo) : (key > klo);
+    m += above ? wunpack(wq[i]) : 0ull;
+    tc += (jties != 0xffffffffu && wq[i] && key == klo) ? 1u : 0u;
+  }
+  u32 ttot;
+  u64 mtot;
+  block_excl2(tc, m, L.s, &ttot, &mtot);
+  if (threadIdx.x == 0) {
+    L.s.r[10] = 0xffffffffu;
+    L.s.r[11] = 0xffffffffu;
+  }
+  lds_sync();
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) {
+    const u32 key = (u32)(ent[i] >> 32);
+    const bool above = jties == 0xffffffffu ? (key >= klo) : (key > klo);
+    const bool tie = jties != 0xffffffffu && wq[i] && key == klo;
+    const u64 before = m + (u64)min(tc, jties == 0xffffffffu ? 0u : jties) * wt;
+    m += above ? wunpack(wq[i]) : 0ull;
+    tc += tie ? 1u : 0u;
+    const u64 after = m + (u64)min(tc, jties == 0xffffffffu ? 0u : jties) * wt;
+    if (before <= t && t < after) L.s.r[10] = (u32)ent[i];
+    if (tie && tc == jties) L.s.r[11] = (u32)ent[i];
+  }
+  lds_sync();
+  const u32 pick = L.s.r[10];
+  const u32 idlo = jties == 0xffffffffu ? (u32)a.V : L.s.r[11];
+  if (pick == 0xffffffffu) return false;
+  write_result(a, row, p, (long long)pick, W, thr, kPathTopK, 0u, kmax, klo, idlo, kept);
+  return true;
+}
+
+// Bin of the mass histogram: linear in -d = q* - q past an offset d0 (bin 0
+// holds the largest keys), clamped to [0, kNB), monotone in the key.
+__device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, float d0, float scale) {
+  const float d = (k == ks) ? 0.0f : q - qs;
+  return min((u32)kNB - 1u, (u32)fmaxf(0.0f, (-d - d0) * scale));
+}
+// Per-row data of top-k-off rows: bin masses [G][kNB] u64, bin counts [G][kNB]
+// u32, then the listed tokens [G][kLC].
+__device__ __forceinline__ u64* list_base(const Args& a, int row) {
+  return row_data(a, row) + (size_t)a.G * kNB + (size_t)a.G * kNB / 2;
+}
+
+// ---------------------------------------------------------------- the streaming kernel
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_sample(Args a) {
+  __shared__ Lds L;
+  constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
+  const int c = blockIdx.x;
+  const int row = a.order ? a.order[blockIdx.y] : (int)blockIdx.y;
+  if ((unsigned)row >= (unsigned)a.B) return;  // row_order must be a permutation of [0, B)
+  Chunk<DT> ch;
+  load_chunk<DT>(a, row, c, ch);
+  const RowP p = row_params(a, row);
+  RowSync* sy = &a.sync[row];
+  Slot* sl = row_slots(a, row);
+  if (p.pen) pen_build(p, c, L);
+
+  if (p.kind == kKindGreedy) {
+    u64 best = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < VL; ++e) {
+        const float z = elem_z(ch, p, L, c, j, e);
+        const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+        best = pk > best ? pk : best;
+      }
+    if (p.pen) lds_sync();
+    best = block_max64(best, L.s);
+    if (threadIdx.x == 0) stc(&sl[c].a, best);
+    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+    finish_greedy(a, p, row, L);
+    reset_row(a, row);
+    return;
+  }
+
+  if (p.kind == kKindTopK) {
+    // z keys
+    u32 kz[E];
+    u32 m = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < VL; ++e) {
+        const u32 kx = ch.valid(j, e) ? skey(elem_z(ch, p, L, c, j, e)) : 0u;
+        kz[j * VL + e] = kx;
+        m = max(m, kx);
+      }
+    if (p.pen) lds_sync();
+    // quota of the chunk and of each wave
+    const int vin = min(kCH, a.V - c * kCH);
+    const int nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
+    const float mu = (float)p.k * (float)kCH / (float)a.V;
+    int kc = (int)ceilf(mu + 4.0f * sqrtf(mu) + 2.0f);
+    kc = min(kc, p.k);
+    const int kw = min(64, max(1, (kc + nw - 1) / nw));
+    // the kw-th largest per-thread maximum of the wave
+    u32 tw = 0;
+    for (int b = 31; b >= 0; --b) {
+      const u32 cand = tw | (1u << b);
+      if ((int)popc64(__ballot(m >= cand)) >= kw) tw = cand;
+    }
+    const bool wave_live = wave_id() < nw;
+    if (lane_id() == 0) L.s.v[wave_id()][4] = wave_live ? tw : 0xffffffffu;
+    lds_sync();
+    u32 tau = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) tau = min(tau, L.s.v[i][4]);
+    tau = max(tau, 1u);
+    lds_sync();
+    const int R = a.R;
+    u32 n = 0;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+      // positions in id order: (wave, j, lane, e)
+      u32 cnt[J];
+      u32 tot = 0;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        u32 x = 0;
+#pragma unroll
+        for (int e = 0; e < VL; ++e) x += kz[j * VL + e] >= tau ? 1u : 0u;
+        cnt[j] = x;
+      }
+      u32 ex[J];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const u32 inc = wave_incl_scan(cnt[j]);
+        ex[j] = inc - cnt[j];
+        const u32 tj = readlane(inc, 63);
+        L.s.v[wave_id()][j] = tj;  // same value from every lane
+        tot += tj;
+      }
+      if (lane_id() == 0) L.s.r[wave_id()] = tot;
+      lds_sync();
+      u32 woff = 0;
+      n = 0;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) {
+        woff += i < wave_id() ? L.s.r[i] : 0u;
+        n += L.s.r[i];
+      }
+      u32 joff[J];
+      {
+        u32 run = woff;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          joff[j] = run;
+          run += L.s.v[wave_id()][j];
+        }
+      }
+      lds_sync();
+      if (n > (u32)R || n > (u32)kStageCap) {
+        if (attempt == 0) {
+          tau = tau + 1u;  // ties at tau overflowed the region: strictly above it
+          continue;
+        }
+        n = 0xffffffffu;
+        break;
+      }
+      // stage (local index, z key) in id order, then one entry per thread
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        u32 pos = joff[j] + ex[j];
+#pragma unroll
+        for (int e = 0; e < VL; ++e) {
+          const u32 kx = kz[j * VL + e];
+          if (kx >= tau) {
+            L.u.stage[pos] = ((u64)kx << 32) | (u32)ch.id(j, e);
+            ++pos;
+          }
+        }
+      }
+      lds_sync();
+      u64* reg = row_data(a, row) + (size_t)c * R;
+      for (u32 i = threadIdx.x; i < n; i += kThreads) {
+        const u64 st = L.u.stage[i];
+        const float q = qdiv(f_of_key((u32)(st >> 32)), p.T, p.rT, p.t_one);
+        stc(&reg[i], ((u64)skey(q) << 32) | (u32)st);
+      }
+      break;
+    }
+    // largest z key left out
+    u32 below = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) below = kz[i] < tau ? max(below, kz[i]) : below;
+    below = block_max(below, L.s);
+    if (threadIdx.x == 0) stc(&sl[c].a, ((u64)below << 32) | n);
+    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+    // ---- the row's last workgroup: gather and finish
+    u32* cnt_l = L.cties;
+    u32 below_max = 0, bad = 0;
+    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
+      const u64 v = ldc(&sl[cc].a);
+      const u32 nc = (u32)v;
+      bad |= nc == 0xffffffffu ? 1u : 0u;
+      cnt_l[cc] = nc == 0xffffffffu ? 0u : nc;
+      below_max = max(below_max, (u32)(v >> 32));
+    }
+    below_max = block_max(below_max, L.s);
+    bad = block_max(bad, L.s);
+    u32 why = bad ? kStOverflow : 0u;
+    bool done = false;
+    if (!why) {
+      u64 ent[kFPer];
+      const u32 tot = gather_lists(a, row_data(a, row), R, cnt_l, ent, L);
+      if (tot == 0xffffffffu)
+        why = kStOverflow;
+      else if (finish_topk(a, p, row, L, ent, tot, below_max))
+        done = true;
+      else
+        why = kStIncomplete;
+    }
+    if (!done) resolve_single<DT>(a, p, row, why, L);
+    reset_row(a, row);
+    return;
+  }
+
+  if (p.kind == kKindSingle) {
+    if (p.pen) lds_sync();
+    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+    resolve_single<DT>(a, p, row, 0u, L);
+    reset_row(a, row);
+    return;
+  }
+
+  // ---------------- mass rows (top-k off)
+  u32 kq[E];
+  chunk_qkeys<DT>(ch, p, L, c, kq);
+  if (p.pen) lds_sync();
+  {
+    u32 kmx = 0, kmn = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      kmx = max(kmx, kq[i]);
+      if (kq[i]) kmn = min(kmn, kq[i]);
+    }
+    kmx = block_max(kmx, L.s);
+    kmn = ~block_max(~kmn, L.s);
+    if (threadIdx.x == 0) stc(&sl[c].a, ((u64)kmx << 32) | kmn);
+  }
+  (void)arrive(&sy->barA, L.s);
+  bool ok = wait_count(a, row, &sy->barA, (u32)a.G, L.s);
+  u32 kstar = 0, kmin = 0xffffffffu;
+  if (ok) {
+    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
+      const u64 v = ldc(&sl[cc].a);
+      kstar = max(kstar, (u32)(v >> 32));
+      kmin = min(kmin, (u32)v);
+    }
+    kstar = block_max(kstar, L.s);
+    kmin = ~block_max(~kmin, L.s);
+    if (kstar == 0u) {
+      fail_row(a, row, kStIncomplete);  // no weights: resolved alone
+      ok = false;
+    }
+  }
+  const int SH = a.SH;
+  const u64 thr = ceil_scaled(p.mp, 23 + SH);
+  const float qs = f_of_key(kstar);
+  // bins linear in d = q - q* over [max(q_min, q* - 44.5), q*]
+  float scale = 0.0f;
+  {
+    const float qmin = f_of_key(kmin);
+    const float span = qs - fmaxf(qmin, qs - 44.5f);
+    scale = span > 0x1p-60f ? (float)kNB / span : 0.0f;  // no spread: every token in bin 0
+  }
+  if (ok) {
+    // weights (packed, kept in registers) and the chunk's mass
+    u32 wp[E];
+    u64 Sc = 0;
+    u32 nz = 0, inb = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      u32 x = wpack_of(f_of_key(kq[i]), kq[i], qs, kstar, SH);
+      const u64 w = wunpack(x);
+      x = w >= thr ? x : 0u;
+      wp[i] = x;
+      Sc += x ? w : 0ull;
+      nz += x ? 1u : 0u;
+      inb |= (x ? 1u : 0u) << i;
+    }
+    Sc = block_sum64(Sc, L.s);
+    nz = block_sum(nz, L.s);
+    if (threadIdx.x == 0) {
+      stc(&sl[c].b, Sc);
+      stc(&sl[c].c, (u64)nz);
+    }
+    if (p.topp) {
+      // Bracket the top-p boundary: each round histograms the tokens still in
+      // the bracket into kNB bins linear in d, the last workgroup to arrive
+      // (the reducer) picks the bin holding the boundary and either lists it
+      // (small enough) or has every workgroup split it again.
+      u32 abv = 0;  // tokens above the bracket
+      float d0 = 0.0f, sc = scale;
+      u64* hm_g = row_data(a, row);
+      u32* hc_g = (u32*)(row_data(a, row) + (size_t)a.G * kNB);
+      bool listed = false;
+      for (int r = 0; r < kRounds && ok && !listed; ++r) {
+        for (int b = threadIdx.x; b < kNB; b += kThreads) {
+          L.u.mh[b] = 0ull;
+          L.hc[b] = 0u;
+        }
+        lds_sync();
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          if ((inb >> i) & 1u) {
+            const u32 b = mass_bin(f_of_key(kq[i]), kq[i], qs, kstar, d0, sc);
+            atomicAdd(&L.u.mh[b], wunpack(wp[i]));
+            atomicAdd(&L.hc[b], 1u);
+          }
+        }
+        lds_sync();
+        for (int b = threadIdx.x; b < kNB; b += kThreads) {
+          stc(&hm_g[(size_t)c * kNB + b], L.u.mh[b]);
+          stc(&hc_g[(size_t)c * kNB + b], L.hc[b]);
+        }
+        const u32 before = arrive(&sy->barB, L.s);
+        if (before == (u32)a.G * (u32)(r + 1) - 1u) {
+          // the reducer: bin totals, per-chunk maxima of the counts, the crossing bin
+          u64 bm = 0;
+          u32 bc = 0, bx = 0;
+          const int b = threadIdx.x;  // kNB == kThreads
+          int cc = 0;
+          for (; cc + 8 <= a.G; cc += 8) {
+            u64 vm[8];
+            u32 vc[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              vm[i] = ldc(&hm_g[(size_t)(cc + i) * kNB + b]);
+              vc[i] = ldc(&hc_g[(size_t)(cc + i) * kNB + b]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              bm += vm[i];
+              bc += vc[i];
+              bx = max(bx, vc[i]);
+            }
+          }
+          for (; cc < a.G; ++cc) {
+            bm += ldc(&hm_g[(size_t)cc * kNB + b]);
+            const u32 v = ldc(&hc_g[(size_t)cc * kNB + b]);
+            bc += v;
+            bx = max(bx, v);
+          }
+          u64 tot;
+          const u64 ex = block_excl64(bm, L.s, &tot);
+          u64 Tp, A;
+          if (r == 0) {
+            Tp = mul_frac(tot, p.tp);
+            A = 0;
+          } else {
+            Tp = ldc(&a.res[row].Tp);
+            A = ldc(&a.res[row].Ahi);
+          }
+          const u64 target = Tp - A;
+          if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
+          lds_sync();
+          if (ex <= target && target < ex + bm) {
+            L.s.r[12] = (u32)b;
+            L.s.r64[12] = ex;
+            L.s.r[13] = bc;
+            L.s.r[14] = bx;
+          }
+          lds_sync();
+          const u32 bsel = L.s.r[12];
+          if (threadIdx.x == 0) {
+            RowRes* rr = &a.res[row];
+            u32 act;  // 1: list the bin, 0: split it again, 2: give up (the exact path resolves the row)
+            if (bsel == 0xffffffffu) {
+              act = 2;
+            } else {
+              const bool small = L.s.r[13] <= (u32)kFCap && L.s.r[14] <= (u32)kLC;
+              act = small ? 1u : (r + 1 < kRounds ? 0u : 2u);
+              if (r == 0) {
+                stc(&rr->Tp, Tp);
+                stc(&rr->S, tot);
+              }
+              stc(&rr->Ahi, A + L.s.r64[12]);
+            }
+            if (act == 2) orc(&sy->status, kStList);
+            wait_mem();
+            stc(&sy->dec, ((u32)(r + 1) << 16) | (act << 14) | (bsel & 0x3fffu));
+          }
+          lds_sync();
+        } else {
+          ok = wait_count(a, row, &sy->dec, (u32)(r + 1) << 16, L.s);
+        }
+        if (ok) {
+          if (threadIdx.x == 0) L.s.r[15] = ldc(&sy->dec);
+          lds_sync();
+          const u32 dv = L.s.r[15];
+          lds_sync();
+          const u32 act = (dv >> 14) & 3u, bsel = dv & 0x3fffu;
+          if (act == 2u) {
+            ok = false;
+          } else {
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+              if ((inb >> i) & 1u) {
+                const u32 b = mass_bin(f_of_key(kq[i]), kq[i], qs, kstar, d0, sc);
+                if (b < bsel) abv |= 1u << i;
+                if (b != bsel) inb &= ~(1u << i);
+              }
+            }
+            listed = act == 1u;
+            d0 = d0 + (float)bsel / sc;
+            sc = sc * (float)kNB;
+          }
+        }
+      }
+      if (ok) {
+        // mass above the bracket, and the bracket's tokens listed in id order
+        u64 above = 0;
+        u32 cnt[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) cnt[j] = 0;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          above += ((abv >> i) & 1u) ? wunpack(wp[i]) : 0ull;
+          cnt[i / VL] += (inb >> i) & 1u;
+        }
+        above = block_sum64(above, L.s);
+        const u32 na = block_sum((u32)__popc(abv), L.s);
+        u32 ex[J], tot = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const u32 inc = wave_incl_scan(cnt[j]);
+          ex[j] = inc - cnt[j];
+          const u32 tj = readlane(inc, 63);
+          L.s.v[wave_id()][j] = tj;
+          tot += tj;
+        }
+        if (lane_id() == 0) L.s.r[wave_id()] = tot;
+        lds_sync();
+        u32 woff = 0, nl = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+          woff += i < wave_id() ? L.s.r[i] : 0u;
+          nl += L.s.r[i];
+        }
+        u32 joff[J];
+        {
+          u32 run = woff;
+#pragma unroll
+          for (int j = 0; j < J; ++j) {
+            joff[j] = run;
+            run += L.s.v[wave_id()][j];
+          }
+        }
+        lds_sync();
+        u64* lst = list_base(a, row) + (size_t)c * kLC;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          u32 pos = joff[j] + ex[j];
+#pragma unroll
+          for (int e = 0; e < VL; ++e) {
+            const int i = j * VL + e;
+            if ((inb >> i) & 1u) {
+              stc(&lst[pos], ((u64)kq[i] << 32) | (u32)ch.id(j, e));
+              ++pos;
+            }
+          }
+        }
+        if (threadIdx.x == 0) {
+          stc(&sl[c].b, above);
+          stc(&sl[c].c, ((u64)nl << 32) | na);
+        }
+      }
+    }
+  }
+  if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+  // ---- the row's last workgroup: the selector
+  const u32 st = ldc(&sy->status);
+  if (st != 0u || kstar == 0u) {
+    resolve_single<DT>(a, p, row, st ? st : kStIncomplete, L);
+    reset_row(a, row);
+    return;
+  }
+  // per-chunk kept masses and tie counts in L.cmass / L.cties
+  u64 W = 0, Tp = 0, A = 0, wt = 0;
+  u32 klo = 1u, jties = 0xffffffffu, kept = 0, idlo = (u32)a.V;
+  bool fine = true;
+  if (!p.topp) {
+    u32 nzt = 0;
+    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
+      L.cmass[cc] = ldc(&sl[cc].b);
+      nzt += (u32)ldc(&sl[cc].c);
+      L.cties[cc] = 0u;
+    }
+    kept = block_sum(nzt, L.s);
+  } else {
+    Tp = ldc(&a.res[row].Tp);
+    const u64 Ahi = ldc(&a.res[row].Ahi);
+    u32 nat = 0;
+    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
+      const u64 cv = ldc(&sl[cc].c);
+      L.cmass[cc] = ldc(&sl[cc].b);
+      L.coff[cc] = 0;
+      L.cties[cc] = (u32)(cv >> 32);  // listed counts, for the gather
+      nat += (u32)cv;
+    }
+    nat = block_sum(nat, L.s);
+    u64 ent[kFPer];
+    const u32 n = gather_lists(a, list_base(a, row), kLC, L.cties, ent, L);
+    if (n == 0xffffffffu || n == 0u) {
+      fine = false;
+    } else {
+      // weights of the listed tokens and the exact boundary inside the bin
+      u32 wq[kFPer];  // packed weights
+      u32 bkmax = 0, bkmin = 0xffffffffu;
+#pragma unroll
+      for (int i = 0; i < kFPer; ++i) {
+        const u32 key = (u32)(ent[i] >> 32);
+        const bool in = threadIdx.x * kFPer + i < n;
+        u32 x = in ? wpack_of(f_of_key(key), key, qs, kstar, SH) : 0u;
+        x = wunpack(x) >= thr ? x : 0u;
+        wq[i] = x;
+        if (in) {
+          bkmax = max(bkmax, key);
+          bkmin = min(bkmin, key);
+        }
+      }
+      bkmax = block_max(bkmax, L.s);
+      bkmin = ~block_max(~bkmin, L.s);
+      Sel q;
+      sel_init(q, bkmin, bkmax, true, Tp - Ahi);
+      for (;;) {
+        sel_clear(L);
+        lds_sync();
+#pragma unroll
+        for (int i = 0; i < kFPer; ++i)
+          if (wq[i]) sel_add(q, L, (u32)(ent[i] >> 32), wunpack(wq[i]));
+        lds_sync();
+        if (sel_step(q, L)) break;
+      }
+      if (q.found != 1) {
+        fine = false;
+      } else {
+        klo = q.kappa;
+        wt = q.kmass / q.kcount;
+        A = Ahi + q.above_m;
+        const u64 jj = (Tp - A) / wt + 1ull;
+        jties = (u32)(jj < (u64)q.kcount ? jj : (u64)q.kcount);
+        W = A + (u64)jties * wt;
+        kept = nat + q.above_c + jties;
+        // per chunk: listed mass above kappa_p and ties at it; the jties-th tie's id
+        for (int cc = threadIdx.x; cc < a.G; cc += kThreads) L.cties[cc] = 0u;
+        lds_sync();
+        u32 tcount = 0;
+#pragma unroll
+        for (int i = 0; i < kFPer; ++i) {
+          const u32 key = (u32)(ent[i] >> 32);
+          const int cc = (int)((u32)ent[i] / (u32)kCH);
+          if (wq[i] && key > klo) atomicAdd(&L.cmass[cc], wunpack(wq[i]));
+          if (wq[i] && key == klo) {
+            atomicAdd(&L.cties[cc], 1u);
+            ++tcount;
+          }
+        }
+        // id of the jties-th tie in id order (the list is in id order, thread-contiguous)
+        u32 tex, ttot;
+        tex = block_excl(tcount, L.s, &ttot);
+        if (threadIdx.x == 0) L.s.r[14] = (u32)a.V;
+        lds_sync();
+#pragma unroll
+        for (int i = 0; i < kFPer; ++i) {
+          const u32 key = (u32)(ent[i] >> 32);
+          if (wq[i] && key == klo) {
+            ++tex;
+            if (tex == jties) L.s.r[14] = (u32)ent[i];
+          }
+        }
+        lds_sync();
+        idlo = L.s.r[14];
+      }
+    }
+  }
+  if (!fine) {
+    resolve_single<DT>(a, p, row, kStList, L);
+    reset_row(a, row);
+    return;
+  }
+  if (!p.topp) {
+    u64 tot = 0;
+    for (int cc = 0; cc < a.G; ++cc) tot += L.cmass[cc];
+    W = tot;
+  }
+  // the chunk holding the draw: kept(c) = cmass[c] + min(ties(c), jties left) * wt
+  const u64 t = mul_frac(W, p.u);
+  if (threadIdx.x == 0) {
+    u64 acc = 0;
+    u32 tb = 0;
+    int owner = -1;
+    u64 tin = 0;
+    u32 jl_owner = 0;
+    for (int cc = 0; cc < a.G; ++cc) {
+      const u32 tcn = L.cties[cc];
+      const u32 jl = jties == 0xffffffffu ? 0u : (jties > tb ? jties - tb : 0u);
+      const u64 kc = L.cmass[cc] + (u64)min(tcn, jl) * wt;
+      if (owner < 0 && t < acc + kc) {
+        owner = cc;
+        tin = t - acc;
+        jl_owner = jl;
+      }
+      acc += kc;
+      tb += tcn;
+    }
+    L.s.r[15] = (u32)owner;
+    L.s.r64[13] = tin;
+    L.s.r[7] = jl_owner;
+  }
+  lds_sync();
+  const int owner = (int)L.s.r[15];
+  const u64 tin = L.s.r64[13];
+  const u32 jl = L.s.r[7];
+  lds_sync();
+  if (owner < 0) {
+    resolve_single<DT>(a, p, row, kStIncomplete, L);
+    reset_row(a, row);
+    return;
+  }
+  // re-read the owner chunk and locate the token
+  load_chunk<DT>(a, row, owner, ch);
+  if (p.pen) pen_build(p, owner, L);
+  chunk_qkeys<DT>(ch, p, L, owner, kq);
+  if (p.pen) lds_sync();
+  const bool ties_on = jties != 0xffffffffu;
+  auto kw = [&](int i) -> KW {
+    u64 w = weight_of(f_of_key(kq[i]), kq[i], qs, kstar, SH);
+    w = w >= thr ? w : 0ull;
+    const bool above = ties_on ? kq[i] > klo : true;
+    return KW{above ? w : 0ull, ties_on && w && kq[i] == klo};
+  };
+  const int pick = chunk_locate<DT>(ch, kw, wt, jl, tin, L);
+  if (pick < 0) {
+    resolve_single<DT>(a, p, row, kStIncomplete, L);
+  } else {
+    write_result(a, row, p, pick, W, thr, p.topp ? kPathMassTopP : kPathMassAll, 0u, kstar, p.topp ? klo : 1u,
+                 p.topp ? idlo : (u32)a.V, kept);
+  }
+  reset_row(a, row);
+}
+
+// ---------------------------------------------------------------- post-filter probabilities
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_probs(Args a) {
+  __shared__ Lds L;
+  const int c = blockIdx.x;
+  const int row = blockIdx.y;
+  Chunk<DT> ch;
+  load_chunk<DT>(a, row, c, ch);
+  const RowP p = row_params(a, row);
+  const RowRes r = a.res[row];
+  float* out = a.out_probs + (size_t)row * a.V;
+  if (p.kind == kKindGreedy) {
+#pragma unroll
+    for (int j = 0; j < Chunk<DT>::J; ++j)
+#pragma unroll
+      for (int e = 0; e < Chunk<DT>::VL; ++e)
+        if (ch.valid(j, e)) out[ch.id(j, e)] = ch.id(j, e) == (int)r.id ? 1.0f : 0.0f;
+    return;
+  }
+  if (p.pen) pen_build(p, c, L);
+  u32 kq[kEPT];
+  chunk_qkeys<DT>(ch, p, L, c, kq);
+  const float qs = f_of_key(r.kstar);
+  const double Wd = (double)r.W;
+#pragma unroll
+  for (int j = 0; j < Chunk<DT>::J; ++j)
+#pragma unroll
+    for (int e = 0; e < Chunk<DT>::VL; ++e) {
+      if (!ch.valid(j, e)) continue;
+      const int i = j * Chunk<DT>::VL + e;
+      const int id = ch.id(j, e);
+      u64 w = r.kstar ? weight_of(f_of_key(kq[i]), kq[i], qs, r.kstar, a.SH) : 0ull;
+      w = w >= r.thr ? w : 0ull;
+      const bool kept = kq[i] > r.klo || (kq[i] == r.klo && (u32)id <= r.idlo);
+      out[id] = (kept && w && r.W) ? (float)((double)w / Wd) : 0.0f;
+    }
+}
+
+__global__ void k_zero(u32* p, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+}  // namespace qs

@@ -20,7 +20,7 @@ def to_device(w, device):
                 history=t(w.history, torch.int32))
 
 
-def run_gpu(w, device, step=0, want_probs=True, all_greedy=False, use_top_p=True, ws=None):
+def run_gpu(w, device, step=0, want_probs=True, all_greedy=False, use_top_p=True, ws=None, order=None, **extra):
     d = to_device(w, device)
     B, V = d["logits"].shape
     H = 0 if d["history"] is None else d["history"].shape[1]
@@ -30,8 +30,10 @@ def run_gpu(w, device, step=0, want_probs=True, all_greedy=False, use_top_p=True
     probs = torch.empty((B, V), dtype=torch.float32, device=device) if want_probs else None
     kept = torch.empty(B, dtype=torch.int32, device=device) if want_probs else None
     logits = d.pop("logits")
-    sample_into(logits, ids, ws, uniforms=u, all_greedy=all_greedy, use_top_p=use_top_p, mass_rows=w.mass_rows,
-                out_probs=probs, out_kept=kept, **d)
+    if order is not None:
+        extra["row_order"] = torch.from_numpy(np.ascontiguousarray(order, dtype=np.int32)).to(device)
+    sample_into(logits, ids, ws, uniforms=u, all_greedy=all_greedy, use_top_p=use_top_p,
+                out_probs=probs, out_kept=kept, **d, **extra)
     torch.cuda.synchronize()
     return (ids.cpu().numpy(), None if probs is None else probs.cpu().numpy(),
             None if kept is None else kept.cpu().numpy())
@@ -41,10 +43,23 @@ def run_oracle(w, step=0, want_probs=True):
     return contract.sample_workload(w, step=step, want_probs=want_probs)
 
 
-# Per-row resolution record of the last call, from the row control blocks at
-# the start of the workspace (256 bytes per row): word 30 is the path (0
-# greedy, 1 top-k, 2 flat mass row, 3 single workgroup, 4 peaked mass row),
-# word 32 the reason a row went to the single-workgroup path (0: it did not).
+# Per-row resolution record of the last call.  The workspace starts with the
+# row counters (640 bytes per row of the workspace's maximum batch), then the
+# row results (128 bytes per row): word 13 is the path (1 greedy, 2 top-k,
+# 3 top-k-off with top-p, 4 top-k-off without, 5 single workgroup), word 14 the
+# reason a row went to the single-workgroup path (0: it did not).
 def row_paths(ws, B):
-    raw = ws.buf[: B * 256].cpu().numpy().view(np.uint32).reshape(B, 64)
-    return raw[:, 30].copy(), raw[:, 32].copy()
+    off = (ws.max_bs * 640 + 255) // 256 * 256
+    raw = ws.buf[off: off + B * 128].cpu().numpy().view(np.uint32).reshape(B, 32)
+    return raw[:, 13].copy(), raw[:, 14].copy()
+
+
+def order_of(T, K, V):
+    """The dispatch order SamplingBatch stages: top-k-off rows, top-k rows by descending k, greedy rows."""
+    def kind(t, k):
+        if t <= 1e-5:
+            return 2
+        return 1 if 0 < k < V and k <= 1024 else 0
+    K = np.zeros(len(T), np.int32) if K is None else K
+    return np.array([r for _, _, r in sorted((kind(T[r], K[r]), 0 if T[r] <= 1e-5 else -int(K[r]), r)
+                                               for r in range(len(T)))], np.int32)

@@ -72,7 +72,7 @@ def main():
         res = contract.sample_workload(w, want_probs=True)
         out[f"{name}/ids"] = res.ids
         out[f"{name}/kept"] = res.kept
-        out[f"{name}/topk_end"] = res.topk_end
+        out[f"{name}/topk_end"] = res.kend
         out[f"{name}/W_hex"] = np.array([format(x, "x") for x in res.W])
         out[f"{name}/probs_sum"] = res.probs.astype(np.float64).sum(axis=1)
         out[f"{name}/logits_digest"] = np.array([digest(r) for r in w.logits], dtype=np.uint64)

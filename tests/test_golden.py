@@ -30,6 +30,6 @@ def test_workload_rows(name):
     res = contract.sample_workload(w, want_probs=True)
     np.testing.assert_array_equal(res.ids, GOLD[f"{name}/ids"])
     np.testing.assert_array_equal(res.kept, GOLD[f"{name}/kept"])
-    np.testing.assert_array_equal(res.topk_end, GOLD[f"{name}/topk_end"])
+    np.testing.assert_array_equal(res.kend, GOLD[f"{name}/topk_end"])
     assert [format(x, "x") for x in res.W] == list(GOLD[f"{name}/W_hex"])
     np.testing.assert_allclose(res.probs.astype(np.float64).sum(axis=1), GOLD[f"{name}/probs_sum"], rtol=0, atol=0)

@@ -9,7 +9,7 @@ from qedge_amd import workloads as W
 from qedge_amd.batch import SamplingBatch
 from qedge_amd.sampler import BatchSampler, Workspace, argmax_into, sample_gpu, sample_into
 from qedge_amd.sampling_params import SamplingParams
-from tests.devrun import row_paths, run_gpu, run_oracle
+from tests.devrun import order_of, row_paths, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -28,19 +28,22 @@ def _dev_logits(x, dtype, device, stride=None):
 
 
 def _run(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hist=None, u=None,
-         use_top_p=True, mass_rows=True, stride=None, probs=True, paths=None):
+         use_top_p=True, stride=None, probs=True, paths=None, min_p=None, order=False, no_wait=False, ws=None,
+         all_greedy=False):
     B, V = x.shape
     lg = _dev_logits(x, dtype, device, stride)
     t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)
     H = 0 if hist is None else hist.shape[1]
-    ws = Workspace(B, V, lg.dtype, H, device)
+    ws = ws or Workspace(B, V, lg.dtype, H, device)
     ids = torch.empty(B, dtype=torch.int64, device=device)
+    ro = t(order_of(T, K, V), torch.int32) if order else None
     pr = torch.empty((B, V), dtype=torch.float32, device=device) if probs else None
     kept = torch.empty(B, dtype=torch.int32, device=device) if probs else None
     sample_into(lg, ids, ws, temperatures=t(T, torch.float32), top_ps=t(P, torch.float32), top_ks=t(K, torch.int32),
                 repetition_penalties=t(rep, torch.float32), presence_penalties=t(pres, torch.float32),
                 frequency_penalties=t(freq, torch.float32), history=t(hist, torch.int32),
-                uniforms=t(u, torch.float32), use_top_p=use_top_p, mass_rows=mass_rows, out_probs=pr, out_kept=kept)
+                uniforms=t(u, torch.float32), use_top_p=use_top_p, out_probs=pr, out_kept=kept,
+                min_ps=t(min_p, torch.float32), row_order=ro, no_wait=no_wait, all_greedy=all_greedy)
     torch.cuda.synchronize()
     if paths is not None:
         paths.extend(row_paths(ws, B))
@@ -50,8 +53,9 @@ def _run(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hi
 def _check(x, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hist=None, u=None, **kw):
     ids, probs, kept = _run(x, dtype, device, T, P, K, rep, pres, freq, hist, u, **kw)
     use_top_p = kw.get("use_top_p", True)
-    ref = contract.sample(x, dtype, T, P if use_top_p else None, K, rep, pres, freq, hist, u,
-                          want_probs=probs is not None)
+    Tref = np.zeros_like(T) if kw.get("all_greedy") else T
+    ref = contract.sample(x, dtype, Tref, P if use_top_p else None, K, rep, pres, freq, hist, u,
+                          want_probs=probs is not None, min_p=kw.get("min_p"))
     np.testing.assert_array_equal(ids, ref.ids)
     if probs is not None:
         np.testing.assert_array_equal(kept, ref.kept)
@@ -137,16 +141,30 @@ def test_penalties_with_padding_ids(gpu):
     _check(W.bf16_bits(x), "bf16", gpu, T, P, K, rep, pres, freq, hist, u)
 
 
-def test_mass_rows_without_the_mass_launch(gpu):
-    """A top-k-off row under the no-mass-rows hint is still exact (slower path)."""
-    rng = np.random.default_rng(5)
-    B, V = 3, 40000
-    x = rng.standard_normal((B, V)).astype(np.float32)
-    T = np.ones(B, np.float32)
-    P = np.array([0.9, 0.9, 0.9], np.float32)
-    K = np.array([20, 0, 50], np.int32)
-    print("[edge] no-mass hint", flush=True)
-    _check(x, "f32", gpu, T, P, K, u=rng.random(B).astype(np.float32), mass_rows=False)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_barrier_timeouts_take_the_exact_path(gpu, dtype):
+    """With QS_FLAG_NO_WAIT every row barrier gives up at once (a host-forced
+    time-out; every kernel still exits normally): the top-k-off rows are then
+    resolved by the exact single-workgroup path, with the same results."""
+    rng = np.random.default_rng(15)
+    B, V = 6, 60000
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    T = np.array([1.0, 0.8, 0.0, 1.2, 0.6, 1.0], np.float32)
+    P = np.array([0.9, 1.0, 1.0, 0.95, 0.7, 0.5], np.float32)
+    K = np.array([0, 0, 0, 0, 40, 0], np.int32)
+    hist = rng.integers(0, V, (B, 300)).astype(np.int32)
+    rep = np.full(B, 1.2, np.float32)
+    pres = np.full(B, 0.3, np.float32)
+    freq = np.full(B, 0.2, np.float32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] barrier time-outs {dtype}", flush=True)
+    paths = []
+    _check(xx, dtype, gpu, T, P, K, rep, pres, freq, hist, u=u, no_wait=True, paths=paths)
+    path, why = paths
+    mass = [0, 1, 3, 5]
+    assert np.all(path[mass] == 5) and np.all(why[mass] != 0), (path.tolist(), why.tolist())
+    assert path[2] == 1 and path[4] == 2
 
 
 def test_adversarial_layout_falls_back_exactly(gpu):
@@ -211,8 +229,7 @@ def test_graph_replays_match_eager(gpu):
 
     def steps():
         for s in range(3):
-            sample_into(lg, outs[s], ws, temperatures=T, top_ps=P, top_ks=K, uniforms=U[s], use_top_p=True,
-                        mass_rows=True)
+            sample_into(lg, outs[s], ws, temperatures=T, top_ps=P, top_ks=K, uniforms=U[s], use_top_p=True)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -268,10 +285,9 @@ def test_special_values_in_top_keys(gpu, dtype):
 @pytest.mark.parametrize("B,V,dtype", [(1, 248320, "bf16"), (2, 2048 * 7 + 100, "bf16"), (3, 600001, "bf16"),
                                        (12, 8192 * 5 + 300, "f32")])
 def test_chunk_layouts_and_sparse_last_chunks(gpu, B, V, dtype):
-    """Batches of up to 8 rows use 2048-logit chunks unless V needs more than
-    256 of them; larger batches use 8192.  A last chunk holding fewer logits
-    than one wave's share leaves waves without tokens; every row must still
-    be resolved on its fast path (no single-workgroup fallback)."""
+    """Rows of 8192-logit chunks whose last chunk holds fewer logits than one
+    wave's share (waves without tokens); every row must still be resolved on
+    its fast path (no single-workgroup fallback)."""
     rng = np.random.default_rng(B * 1000 + V % 997)
     x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
     x[0, V - 7] = 9.0  # a top token inside the last chunk
@@ -294,11 +310,9 @@ def test_chunk_layouts_and_sparse_last_chunks(gpu, B, V, dtype):
 
 @pytest.mark.parametrize("B,V,dtype", [(40, 8192 * 6 + 123, "bf16"), (64, 50000, "f32"), (8, 30011, "bf16"),
                                        (6, 20000, "f32")])
-def test_more_mass_rows_than_mass_slots(gpu, B, V, dtype):
-    """Batches of at most 64 rows run in one streaming launch whose first
-    min(B, 8) grid rows take the batch's first mass rows; the other mass rows
-    are streamed from their own grid rows.  Flat, peaked and no-top-p mass
-    rows mixed with top-k and greedy rows, more mass rows than slots."""
+def test_many_top_k_off_rows(gpu, B, V, dtype):
+    """Flat, peaked and no-top-p rows with top-k off, mixed with top-k and
+    greedy rows, in the natural order and in the dispatch order."""
     rng = np.random.default_rng(B * 7919 + V)
     x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
     xx = W.bf16_bits(x) if dtype == "bf16" else x
@@ -307,9 +321,10 @@ def test_more_mass_rows_than_mass_slots(gpu, B, V, dtype):
     P = np.array([kinds[r % len(kinds)][1] for r in range(B)], np.float32)
     K = np.array([kinds[r % len(kinds)][2] for r in range(B)], np.int32)
     u = rng.random(B).astype(np.float32)
-    print(f"[edge] mass slots B={B} V={V} {dtype}", flush=True)
+    print(f"[edge] top-k-off rows B={B} V={V} {dtype}", flush=True)
     paths = []
     _check(xx, dtype, gpu, T, P, K, u=u, paths=paths)
+    _check(xx, dtype, gpu, T, P, K, u=u, order=True)
     why = paths[1]
     assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
 
@@ -327,23 +342,20 @@ def _mixed_rows(B, V, seed):
 
 @pytest.mark.parametrize("B,V,dtype", [(72, W.VOCAB, "bf16"), (100, W.VOCAB, "f32")])
 def test_mixed_batches_above_64_rows(gpu, B, V, dtype):
-    """Batches above 64 rows run the mass rows and the other rows as two
-    launches on two streams (event fork and join); mixed kinds against the
-    oracle, every row on its fast path at the full vocabulary.  (At small V
-    a top-k of 1000 over bf16 ties can exceed what the per-chunk regions
-    hold; such rows are resolved exactly by the single-workgroup path.)"""
+    """Mixed kinds above 64 rows against the oracle, every row on its fast
+    path at the full vocabulary, with the dispatch order."""
     x, T, P, K, rng = _mixed_rows(B, V, B * 31 + V)
     xx = W.bf16_bits(x) if dtype == "bf16" else x
     u = rng.random(B).astype(np.float32)
-    print(f"[edge] two-stream batch B={B} V={V} {dtype}", flush=True)
+    print(f"[edge] mixed batch B={B} V={V} {dtype}", flush=True)
     paths = []
-    _check(xx, dtype, gpu, T, P, K, u=u, paths=paths)
+    _check(xx, dtype, gpu, T, P, K, u=u, paths=paths, order=True)
     why = paths[1]
     assert not np.any(why), f"rows {np.nonzero(why)[0].tolist()} fell back (reasons {why[why != 0].tolist()})"
 
 
-def test_graph_replays_two_streams(gpu):
-    """Replays of a captured two-stream call (B = 72) match the eager calls."""
+def test_graph_replays_with_row_order(gpu):
+    """Replays of a captured call (B = 72, dispatch order given) match the eager calls."""
     B, V = 72, 8192 * 12 + 77
     x, T, P, K, rng = _mixed_rows(B, V, 4242)
     lg = _dev_logits(W.bf16_bits(x), "bf16", gpu)
@@ -351,14 +363,15 @@ def test_graph_replays_two_streams(gpu):
     Td, Pd, Kd = t(T, torch.float32), t(P, torch.float32), t(K, torch.int32)
     U = [t(rng.random(B).astype(np.float32), torch.float32) for _ in range(2)]
     ws = Workspace(B, V, torch.bfloat16, 0, gpu)
+    ro = t(order_of(T, K, V), torch.int32)
     outs = [torch.empty(B, dtype=torch.int64, device=gpu) for _ in range(2)]
 
     def steps():
         for s in range(2):
             sample_into(lg, outs[s], ws, temperatures=Td, top_ps=Pd, top_ks=Kd, uniforms=U[s], use_top_p=True,
-                        mass_rows=True)
+                        row_order=ro)
 
-    print("[edge] graph replays, two streams", flush=True)
+    print("[edge] graph replays with a row order", flush=True)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):

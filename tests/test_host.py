@@ -67,7 +67,9 @@ def test_batch_normalises_like_the_reference():
     assert np.all((u >= 0) & (u < 1))
     assert u[4] == seeded_uniforms(np.array([7], np.uint64), 0)[0]
     kw = b.sampler_kwargs()
-    assert kw["history"].shape == (bs, 4) and kw["mass_rows"] is True
+    assert kw["history"].shape == (bs, 4) and kw["min_ps"].shape == (bs,)
+    # dispatch order: top-k-off rows first, then top-k rows by descending k, greedy rows last
+    np.testing.assert_array_equal(b.row_order[:bs].numpy(), [2, 3, 4, 1, 0])
 
 
 def test_batch_flags_for_fast_topk_batches():
@@ -148,15 +150,16 @@ def test_library_exports_every_declared_function():
     assert lib.qs_version() >= 200
 
 
-def test_workspace_size_grows_with_batch_and_history():
+def test_workspace_size_grows_with_batch_only():
     from qedge_amd import _lib
 
     lib = _lib.load()
     a = lib.qs_workspace_bytes(1, 248320, 1, 0)
     b = lib.qs_workspace_bytes(64, 248320, 1, 0)
-    c = lib.qs_workspace_bytes(64, 248320, 1, 4096)
-    assert 0 < a < b <= c
+    c = lib.qs_workspace_bytes(64, 248320, 0, 4096)
+    assert 0 < a < b == c
     assert a % 256 == 0 and b % 256 == 0
+    assert lib.qs_workspace_bytes(1, 0, 1, 0) == 0
 
 
 def test_argument_errors_are_reported_without_a_gpu():
@@ -165,18 +168,18 @@ def test_argument_errors_are_reported_without_a_gpu():
     lib = _lib.load()
     P = ctypes.c_void_p
     # null workspace / bad dtype / bad shape: rejected before any launch
-    rc = lib.qs_sample(P(1), 100, 7, 1, 100, P(1), None, None, None, None, None, None, 0, P(1), 0, P(1),
-                       None, None, P(256), 1 << 20, None)
-    assert rc < 0 and b"dtype" in lib.qs_last_error()
-    rc = lib.qs_sample(P(1), 50, 0, 1, 100, P(1), None, None, None, None, None, None, 0, P(1), 0, P(1),
-                       None, None, P(256), 1 << 20, None)
-    assert rc < 0 and b"row_stride" in lib.qs_last_error()
-    rc = lib.qs_sample(P(1), 100, 0, 1, 100, P(1), None, None, None, None, None, P(1), 9000, P(1), 0, P(1),
-                       None, None, P(256), 1 << 30, None)
-    assert rc < 0 and b"history" in lib.qs_last_error()
-    rc = lib.qs_sample(P(1), 100, 0, 1, 100, None, None, None, None, None, None, None, 0, P(1), 0, P(1),
-                       None, None, P(256), 1 << 20, None)
-    assert rc < 0 and b"temperature" in lib.qs_last_error()
+    def call(stride=100, dtype=0, T=P(1), hist=None, H=0, flags=0, ws_bytes=1 << 20, B=1, V=100):
+        return lib.qs_sample(P(1), stride, dtype, B, V, T, None, None, None, None, None, None, hist, H, None,
+                             P(1), None, flags, P(1), None, None, P(256), ws_bytes, None)
+
+    assert call(dtype=7) < 0 and b"dtype" in lib.qs_last_error()
+    assert call(stride=50) < 0 and b"row_stride" in lib.qs_last_error()
+    assert call(hist=P(1), H=70000) < 0 and b"history" in lib.qs_last_error()
+    assert call(hist=None, H=5) < 0 and b"hist_ids" in lib.qs_last_error()
+    assert call(T=None) < 0 and b"temperature" in lib.qs_last_error()
+    assert call(flags=1 << 9) < 0 and b"flags" in lib.qs_last_error()
+    assert call(ws_bytes=1024) < 0 and b"workspace" in lib.qs_last_error()
+    assert call(B=0) == 0  # an empty batch is a no-op
 
 
 # ---------------------------------------------------------------- bench contract
