@@ -10,7 +10,7 @@ typedef unsigned long long u64;
 typedef uint32_t u32;
 typedef unsigned __int128 u128;
 
-constexpr int kThreads = 256;  // every kernel: 4 waves of 64
+constexpr int kThreads = 512;  // every kernel: 8 waves of 64
 constexpr int kWaves = kThreads / 64;
 
 // ---------------------------------------------------------------- memory model
@@ -38,20 +38,44 @@ __device__ __forceinline__ void wait_mem() {
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
+// Every access to device memory goes through these, with the pointer cast to
+// the global address space: generic (flat) accesses would also count against
+// the LDS wait counter, so each workgroup barrier would wait for them.
+// (The host compilation pass parses these device functions too; it keeps
+// generic pointers.)
+#if defined(__HIP_DEVICE_COMPILE__)
+template <typename T>
+using gptr = __attribute__((address_space(1))) T*;
+#else
+template <typename T>
+using gptr = T*;
+#endif
+template <typename T>
+__device__ __forceinline__ gptr<T> gp(T* p) {
+  return (gptr<T>)p;
+}
+template <typename T>
+__device__ __forceinline__ T gld(const T* p) {
+  return *gp(p);
+}
+template <typename T>
+__device__ __forceinline__ void gst(T* p, T v) {
+  *gp(p) = v;
+}
 template <typename T>
 __device__ __forceinline__ T ldc(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 template <typename T>
 __device__ __forceinline__ void stc(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 template <typename T>
 __device__ __forceinline__ T addc(T* p, T v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void orc(u32* p, u32 v) {
-  __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- wave64 collectives (DPP)

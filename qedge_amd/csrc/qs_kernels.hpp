@@ -30,7 +30,7 @@ constexpr int kWaveSpan = kCH / kWaves;    // contiguous ids per wave
 constexpr int kMaxG = 256;                 // chunks per row
 constexpr int kRegionTotal = 8192;         // top-k candidate entries per row (G * R)
 constexpr int kTopkMax = QS_TOPK_FAST_MAX; // top-k served from candidates
-constexpr int kFPer = 16;                  // gathered entries per finishing thread
+constexpr int kFPer = 4096 / kThreads;     // gathered entries per finishing thread
 constexpr int kFCap = kFPer * kThreads;    // gathered entries per row
 constexpr int kNB = 256;                   // mass histogram bins (one per thread)
 constexpr int kRounds = 3;                 // bracket rounds before the exact path
@@ -39,6 +39,8 @@ constexpr int kNBS = 1024;                 // select histogram bins
 constexpr int kStageCap = 1024;            // entries staged in LDS by one workgroup
 
 enum : u32 { kStOverflow = 1u, kStIncomplete = 2u, kStTimeout = 4u, kStList = 8u };
+constexpr u32 kWhyLargeK = 16u;          // top-k above kTopkMax
+constexpr u32 kNotLast = 0xffffffffu;    // not the row's last workgroup
 enum : u32 { kKindGreedy = 0, kKindTopK = 1, kKindMass = 2, kKindSingle = 3 };
 // How the last call resolved a row (RowRes::path).
 enum : u32 { kPathGreedy = 1, kPathTopK = 2, kPathMassTopP = 3, kPathMassAll = 4, kPathSingle = 5 };
@@ -96,7 +98,19 @@ struct Args {
   Slot* slots;  // [B, kMaxG]
   u64* data;    // [B, data_per_row]
   long long data_per_row;  // u64 entries
+  u64* trace;   // trace builds only: [B, G, 16] phase time stamps
 };
+
+#ifdef QS_TRACE
+#define QS_TR(i)                                                                             \
+  do {                                                                                       \
+    if (a.trace && threadIdx.x == 0) a.trace[((size_t)row * a.G + c) * 16 + (i)] = wall_clock64(); \
+  } while (0)
+#else
+#define QS_TR(i) \
+  do {           \
+  } while (0)
+#endif
 
 struct RowP {
   float T, rT, tp, mp, rep, pres, freq, u;
@@ -107,21 +121,21 @@ struct RowP {
 
 __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   RowP p;
-  p.T = a.temperature ? a.temperature[row] : 0.0f;
+  p.T = a.temperature ? gld(a.temperature + row) : 0.0f;
   const bool greedy = (a.flags & QS_FLAG_ALL_GREEDY) || (p.T <= 1e-5f);
-  p.k = a.top_k ? a.top_k[row] : 0;
+  p.k = a.top_k ? gld(a.top_k + row) : 0;
   const bool topk_on = p.k > 0 && p.k < a.V;
-  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? a.top_p[row] : 1.0f;
+  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? gld(a.top_p + row) : 1.0f;
   p.topp = p.tp < 1.0f;
-  p.mp = a.min_p ? a.min_p[row] : 0.0f;
-  p.rep = a.rep ? a.rep[row] : 1.0f;
-  p.pres = a.pres ? a.pres[row] : 0.0f;
-  p.freq = a.freq ? a.freq[row] : 0.0f;
-  p.hlen = a.hist ? (a.hist_len ? a.hist_len[row] : a.H) : 0;
+  p.mp = a.min_p ? gld(a.min_p + row) : 0.0f;
+  p.rep = a.rep ? gld(a.rep + row) : 1.0f;
+  p.pres = a.pres ? gld(a.pres + row) : 0.0f;
+  p.freq = a.freq ? gld(a.freq + row) : 0.0f;
+  p.hlen = a.hist ? (a.hist_len ? gld(a.hist_len + row) : a.H) : 0;
   if (p.hlen > a.H) p.hlen = a.H;
   p.hist = a.hist ? a.hist + (size_t)row * a.H : nullptr;
   p.pen = p.hist != nullptr && p.hlen > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
-  p.u = a.uniforms ? a.uniforms[row] : 0.0f;
+  p.u = a.uniforms ? gld(a.uniforms + row) : 0.0f;
   if (!(p.u >= 0.0f)) p.u = 0.0f;
   if (p.u >= 1.0f) p.u = __uint_as_float(0x3f7fffffu);
   p.kind = greedy ? kKindGreedy : (topk_on ? (p.k <= kTopkMax ? kKindTopK : kKindSingle) : kKindMass);
@@ -185,21 +199,21 @@ __device__ __forceinline__ void load_chunk(const Args& a, int row, int c, Chunk<
     const int i0 = ch.base + j * 64 * VL;
     if (a.vec_ok && i0 + VL <= a.V) {
       if (DT == QS_DTYPE_F32)
-        ch.v[j] = *(const uint4*)((const float*)a.logits + rowoff + i0);
+        ch.v[j] = gld((const uint4*)((const float*)a.logits + rowoff + i0));
       else
-        ch.v[j] = *(const uint4*)((const uint16_t*)a.logits + rowoff + i0);
+        ch.v[j] = gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
     } else {
       u32 x[4] = {0u, 0u, 0u, 0u};
       if (DT == QS_DTYPE_F32) {
         const float* p = (const float*)a.logits + rowoff;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (i0 + e < a.V) x[e] = __float_as_uint(p[i0 + e]);
+          if (i0 + e < a.V) x[e] = __float_as_uint(gld(p + i0 + e));
       } else {
         const uint16_t* p = (const uint16_t*)a.logits + rowoff;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (i0 + e < a.V) x[e >> 1] |= (u32)p[i0 + e] << ((e & 1) * 16);
+          if (i0 + e < a.V) x[e >> 1] |= (u32)gld(p + i0 + e) << ((e & 1) * 16);
       }
       ch.v[j] = make_uint4(x[0], x[1], x[2], x[3]);
     }
@@ -213,7 +227,7 @@ __device__ __forceinline__ void pen_build(const RowP& p, int c, Lds& L) {
   lds_sync();
   const int lo = c * kCH;
   for (int i = threadIdx.x; i < p.hlen; i += kThreads) {
-    const int d = p.hist[i] - lo;
+    const int d = gld(p.hist + i) - lo;
     if ((unsigned)d < (unsigned)kCH) atomicAdd(&L.u.pen[d >> 1], (d & 1) ? 0x10000u : 1u);
   }
   lds_sync();
@@ -300,19 +314,19 @@ __device__ __forceinline__ Slot* row_slots(const Args& a, int row) { return a.sl
 __device__ __forceinline__ void write_result(const Args& a, int row, const RowP& p, long long id, u64 W, u64 thr,
                                              u32 path, u32 why, u32 kstar, u32 klo, u32 idlo, u32 kept) {
   if (threadIdx.x == 0) {
-    a.out_ids[row] = id;
-    if (a.out_kept) a.out_kept[row] = (int)kept;
+    gst(a.out_ids + row, id);
+    if (a.out_kept) gst(a.out_kept + row, (int)kept);
     RowRes* r = &a.res[row];
-    r->id = id;
-    r->W = W;
-    r->thr = thr;
-    r->kind = (u32)p.kind;
-    r->path = path;
-    r->why = why;
-    r->kstar = kstar;
-    r->klo = klo;
-    r->idlo = idlo;
-    r->kept = kept;
+    gst(&r->id, id);
+    gst(&r->W, W);
+    gst(&r->thr, thr);
+    gst(&r->kind, (u32)p.kind);
+    gst(&r->path, path);
+    gst(&r->why, why);
+    gst(&r->kstar, kstar);
+    gst(&r->klo, klo);
+    gst(&r->idlo, idlo);
+    gst(&r->kept, kept);
   }
 }
 
@@ -513,17 +527,17 @@ __device__ __forceinline__ void chunk_vec(const Args& a, const RowP& p, int row,
   const size_t rowoff = (size_t)row * (size_t)a.row_stride;
   u32 x[4] = {0u, 0u, 0u, 0u};
   if (a.vec_ok && i0 + VL <= a.V) {
-    const uint4 v = DT == QS_DTYPE_F32 ? *(const uint4*)((const float*)a.logits + rowoff + i0)
-                                       : *(const uint4*)((const uint16_t*)a.logits + rowoff + i0);
+    const uint4 v = DT == QS_DTYPE_F32 ? gld((const uint4*)((const float*)a.logits + rowoff + i0))
+                                       : gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
     x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
   } else if (DT == QS_DTYPE_F32) {
     const float* q = (const float*)a.logits + rowoff;
     for (int e = 0; e < 4; ++e)
-      if (i0 + e < a.V) x[e] = __float_as_uint(q[i0 + e]);
+      if (i0 + e < a.V) x[e] = __float_as_uint(gld(q + i0 + e));
   } else {
     const uint16_t* q = (const uint16_t*)a.logits + rowoff;
     for (int e = 0; e < 8; ++e)
-      if (i0 + e < a.V) x[e >> 1] |= (u32)q[i0 + e] << ((e & 1) * 16);
+      if (i0 + e < a.V) x[e >> 1] |= (u32)gld(q + i0 + e) << ((e & 1) * 16);
   }
 #pragma unroll
   for (int e = 0; e < VL; ++e) {
@@ -542,8 +556,10 @@ constexpr int vecs_per_chunk(int DT) { return kCH / (DT == QS_DTYPE_F32 ? 4 : 8)
 // f(z, id) over the whole row (chunk by chunk, penalty table per chunk).
 template <int DT, typename F>
 __device__ __forceinline__ void row_pass(const Args& a, const RowP& p, int row, Lds& L, F&& f) {
+#pragma unroll 1
   for (int c = 0; c < a.G; ++c) {
     if (p.pen) pen_build(p, c, L);
+#pragma unroll 1
     for (int m = 0; m < vecs_per_chunk(DT); ++m)
       chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int id) { f(z, id); });
     if (p.pen) lds_sync();
@@ -551,7 +567,8 @@ __device__ __forceinline__ void row_pass(const Args& a, const RowP& p, int row, 
 }
 
 template <int DT>
-__device__ __noinline__ void resolve_single(const Args& a, const RowP& p, int row, u32 why, Lds& L) {
+__device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, Lds& L) {
+  const RowP p = row_params(a, row);
   const int SH = a.SH;
   const u64 thr = ceil_scaled(p.mp, 23 + SH);
   // pass 1: key range of q over non-NaN tokens, and the greedy id for rows without weights
@@ -640,11 +657,13 @@ __device__ __noinline__ void resolve_single(const Args& a, const RowP& p, int ro
   u64 acc_above = 0;   // the same without the ties (they count through ties_before)
   u32 ties_before = 0;
   int pick = -1, idlo = -1;
+#pragma unroll 1
   for (int c = 0; c < a.G && (pick < 0 || (ties_on && idlo < 0)); ++c) {
     if (p.pen) pen_build(p, c, L);
     // kept mass and ties of the chunk
     u64 cm = 0;
     u32 ct = 0;
+#pragma unroll 1
     for (int m = 0; m < vecs_per_chunk(DT); ++m)
       chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int) {
         u32 k;
@@ -662,7 +681,8 @@ __device__ __noinline__ void resolve_single(const Args& a, const RowP& p, int ro
       // id-order walk of the chunk: vector m of every thread, then m + 1
       u64 run_m = acc_above;
       u32 run_t = ties_before;
-      for (int m = 0; m < vecs_per_chunk(DT); ++m) {
+  #pragma unroll 1
+    for (int m = 0; m < vecs_per_chunk(DT); ++m) {
         u64 vm = 0;
         u32 vt = 0;
         chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int) {
@@ -747,7 +767,8 @@ __device__ __forceinline__ u32 gather_lists(const Args& a, const u64* base, int 
   lds_sync();
   const u32 total = L.coff[a.G];
   if (total > (u32)kFCap) return 0xffffffffu;
-  // thread t: positions f = t*kFPer + i; chunk of the first by binary search
+  // thread t: positions f = t*kFPer + i; chunk of the first by binary search,
+  // then the offsets of all its entries, then every load at once
   const u32 f0 = threadIdx.x * kFPer;
   int c = 0;
   {
@@ -758,12 +779,15 @@ __device__ __forceinline__ u32 gather_lists(const Args& a, const u64* base, int 
     }
     c = lo;
   }
+  u32 off[kFPer];
 #pragma unroll
   for (int i = 0; i < kFPer; ++i) {
     const u32 f = f0 + i;
     while (c < a.G - 1 && L.coff[c + 1] <= f) ++c;
-    ent[i] = f < total ? ldc(base + (size_t)c * stride + (f - L.coff[c])) : 0ull;
+    off[i] = f < total ? (u32)c * (u32)stride + (f - L.coff[c]) : 0xffffffffu;
   }
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) ent[i] = off[i] != 0xffffffffu ? ldc(base + off[i]) : 0ull;
   return total;
 }
 
@@ -774,7 +798,7 @@ __device__ __forceinline__ u32 gather_lists(const Args& a, const u64* base, int 
 // mass above it and Tp the row's target; per-chunk masses above the bin come in
 // L.cmass (already loaded) and the draw target is located to a chunk.
 __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int row, Lds& L, u64 (&ent)[kFPer], u32 n,
-                                            u32 below_max) {
+                                            u32 below_max, int c) {
   const int SH = a.SH;
   const u64 thr = ceil_scaled(p.mp, 23 + SH);
   // key range of the candidates
@@ -789,6 +813,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   }
   kmax = block_max(kmax, L.s);
   kmin = ~block_max(~kmin, L.s);
+  QS_TR(7);
   if (n == 0 || kmax == 0u) return false;
   // kappa_k
   u32 kk;
@@ -816,6 +841,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
       if (kb >= kk) return false;
     }
   }
+  QS_TR(8);
   const float qs = f_of_key(kmax);
   u32 wq[kFPer];  // packed weights
   u64 S = 0;
@@ -834,6 +860,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   nz = block_sum(nz, L.s);
   u32 klo = kk, jties = 0xffffffffu, kept = nz;
   u64 W = S, wt = 0;
+  QS_TR(9);
   if (p.topp) {
     const u64 Tp = mul_frac(S, p.tp);
     Sel q;
@@ -856,6 +883,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
     W = A + (u64)jties * wt;
     kept = q.above_c + jties;
   }
+  QS_TR(10);
   // the draw over the entries in id order (thread-contiguous)
   const u64 t = mul_frac(W, p.u);
   u64 m = 0;
@@ -888,6 +916,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
     if (tie && tc == jties) L.s.r[11] = (u32)ent[i];
   }
   lds_sync();
+  QS_TR(11);
   const u32 pick = L.s.r[10];
   const u32 idlo = jties == 0xffffffffu ? (u32)a.V : L.s.r[11];
   if (pick == 0xffffffffu) return false;
@@ -909,189 +938,166 @@ __device__ __forceinline__ u64* list_base(const Args& a, int row) {
 
 // ---------------------------------------------------------------- the streaming kernel
 
+// Streaming and (in the row's last workgroup) finishing of a top-k row.
+// Returns kNotLast in the other workgroups, else 0 or a reason to resolve the
+// row by the exact single-workgroup path.
 template <int DT>
-__global__ __launch_bounds__(kThreads) void k_sample(Args a) {
-  __shared__ Lds L;
+__device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int row, const int c, Chunk<DT>& ch,
+                                        Lds& L) {
   constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
-  const int c = blockIdx.x;
-  const int row = a.order ? a.order[blockIdx.y] : (int)blockIdx.y;
-  if ((unsigned)row >= (unsigned)a.B) return;  // row_order must be a permutation of [0, B)
-  Chunk<DT> ch;
-  load_chunk<DT>(a, row, c, ch);
-  const RowP p = row_params(a, row);
   RowSync* sy = &a.sync[row];
   Slot* sl = row_slots(a, row);
-  if (p.pen) pen_build(p, c, L);
-
-  if (p.kind == kKindGreedy) {
-    u64 best = 0;
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int e = 0; e < VL; ++e) {
-        const float z = elem_z(ch, p, L, c, j, e);
-        const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
-        best = pk > best ? pk : best;
-      }
-    if (p.pen) lds_sync();
-    best = block_max64(best, L.s);
-    if (threadIdx.x == 0) stc(&sl[c].a, best);
-    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
-    finish_greedy(a, p, row, L);
-    reset_row(a, row);
-    return;
-  }
-
-  if (p.kind == kKindTopK) {
     // z keys
-    u32 kz[E];
-    u32 m = 0;
+  u32 kz[E];
+  u32 m = 0;
 #pragma unroll
-    for (int j = 0; j < J; ++j)
+  for (int j = 0; j < J; ++j)
 #pragma unroll
-      for (int e = 0; e < VL; ++e) {
-        const u32 kx = ch.valid(j, e) ? skey(elem_z(ch, p, L, c, j, e)) : 0u;
-        kz[j * VL + e] = kx;
-        m = max(m, kx);
-      }
-    if (p.pen) lds_sync();
-    // quota of the chunk and of each wave
-    const int vin = min(kCH, a.V - c * kCH);
-    const int nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
-    const float mu = (float)p.k * (float)kCH / (float)a.V;
-    int kc = (int)ceilf(mu + 4.0f * sqrtf(mu) + 2.0f);
-    kc = min(kc, p.k);
-    const int kw = min(64, max(1, (kc + nw - 1) / nw));
-    // the kw-th largest per-thread maximum of the wave
-    u32 tw = 0;
-    for (int b = 31; b >= 0; --b) {
-      const u32 cand = tw | (1u << b);
-      if ((int)popc64(__ballot(m >= cand)) >= kw) tw = cand;
+    for (int e = 0; e < VL; ++e) {
+      const u32 kx = ch.valid(j, e) ? skey(elem_z(ch, p, L, c, j, e)) : 0u;
+      kz[j * VL + e] = kx;
+      m = max(m, kx);
     }
-    const bool wave_live = wave_id() < nw;
-    if (lane_id() == 0) L.s.v[wave_id()][4] = wave_live ? tw : 0xffffffffu;
+  if (p.pen) lds_sync();
+  // quota of the chunk and of each wave
+  const int vin = min(kCH, a.V - c * kCH);
+  const int nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
+  const float mu = (float)p.k * (float)kCH / (float)a.V;
+  int kc = (int)ceilf(mu + 4.0f * sqrtf(mu) + 2.0f);
+  kc = min(kc, p.k);
+  const int kw = min(64, max(1, (kc + nw - 1) / nw));
+  // the kw-th largest per-thread maximum of the wave
+  u32 tw = 0;
+  for (int b = 31; b >= 0; --b) {
+    const u32 cand = tw | (1u << b);
+    if ((int)popc64(__ballot(m >= cand)) >= kw) tw = cand;
+  }
+  const bool wave_live = wave_id() < nw;
+  if (lane_id() == 0) L.s.v[wave_id()][4] = wave_live ? tw : 0xffffffffu;
+  lds_sync();
+  u32 tau = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) tau = min(tau, L.s.v[i][4]);
+  tau = max(tau, 1u);
+  lds_sync();
+  QS_TR(2);
+  const int R = a.R;
+  u32 n = 0;
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    // positions in id order: (wave, j, lane, e)
+    u32 cnt[J];
+    u32 tot = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      u32 x = 0;
+#pragma unroll
+      for (int e = 0; e < VL; ++e) x += kz[j * VL + e] >= tau ? 1u : 0u;
+      cnt[j] = x;
+    }
+    u32 ex[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const u32 inc = wave_incl_scan(cnt[j]);
+      ex[j] = inc - cnt[j];
+      const u32 tj = readlane(inc, 63);
+      L.s.v[wave_id()][j] = tj;  // same value from every lane
+      tot += tj;
+    }
+    if (lane_id() == 0) L.s.r[wave_id()] = tot;
     lds_sync();
-    u32 tau = 0xffffffffu;
+    u32 woff = 0;
+    n = 0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) tau = min(tau, L.s.v[i][4]);
-    tau = max(tau, 1u);
+    for (int i = 0; i < kWaves; ++i) {
+      woff += i < wave_id() ? L.s.r[i] : 0u;
+      n += L.s.r[i];
+    }
+    u32 joff[J];
+    {
+      u32 run = woff;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        joff[j] = run;
+        run += L.s.v[wave_id()][j];
+      }
+    }
     lds_sync();
-    const int R = a.R;
-    u32 n = 0;
-    for (int attempt = 0; attempt < 2; ++attempt) {
-      // positions in id order: (wave, j, lane, e)
-      u32 cnt[J];
-      u32 tot = 0;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        u32 x = 0;
-#pragma unroll
-        for (int e = 0; e < VL; ++e) x += kz[j * VL + e] >= tau ? 1u : 0u;
-        cnt[j] = x;
+    if (n > (u32)R || n > (u32)kStageCap) {
+      if (attempt == 0) {
+        tau = tau + 1u;  // ties at tau overflowed the region: strictly above it
+        continue;
       }
-      u32 ex[J];
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const u32 inc = wave_incl_scan(cnt[j]);
-        ex[j] = inc - cnt[j];
-        const u32 tj = readlane(inc, 63);
-        L.s.v[wave_id()][j] = tj;  // same value from every lane
-        tot += tj;
-      }
-      if (lane_id() == 0) L.s.r[wave_id()] = tot;
-      lds_sync();
-      u32 woff = 0;
-      n = 0;
-#pragma unroll
-      for (int i = 0; i < kWaves; ++i) {
-        woff += i < wave_id() ? L.s.r[i] : 0u;
-        n += L.s.r[i];
-      }
-      u32 joff[J];
-      {
-        u32 run = woff;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-          joff[j] = run;
-          run += L.s.v[wave_id()][j];
-        }
-      }
-      lds_sync();
-      if (n > (u32)R || n > (u32)kStageCap) {
-        if (attempt == 0) {
-          tau = tau + 1u;  // ties at tau overflowed the region: strictly above it
-          continue;
-        }
-        n = 0xffffffffu;
-        break;
-      }
-      // stage (local index, z key) in id order, then one entry per thread
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        u32 pos = joff[j] + ex[j];
-#pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const u32 kx = kz[j * VL + e];
-          if (kx >= tau) {
-            L.u.stage[pos] = ((u64)kx << 32) | (u32)ch.id(j, e);
-            ++pos;
-          }
-        }
-      }
-      lds_sync();
-      u64* reg = row_data(a, row) + (size_t)c * R;
-      for (u32 i = threadIdx.x; i < n; i += kThreads) {
-        const u64 st = L.u.stage[i];
-        const float q = qdiv(f_of_key((u32)(st >> 32)), p.T, p.rT, p.t_one);
-        stc(&reg[i], ((u64)skey(q) << 32) | (u32)st);
-      }
+      n = 0xffffffffu;
       break;
     }
-    // largest z key left out
-    u32 below = 0;
+    // stage (local index, z key) in id order, then one entry per thread
 #pragma unroll
-    for (int i = 0; i < E; ++i) below = kz[i] < tau ? max(below, kz[i]) : below;
-    below = block_max(below, L.s);
-    if (threadIdx.x == 0) stc(&sl[c].a, ((u64)below << 32) | n);
-    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
-    // ---- the row's last workgroup: gather and finish
-    u32* cnt_l = L.cties;
-    u32 below_max = 0, bad = 0;
-    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
-      const u64 v = ldc(&sl[cc].a);
-      const u32 nc = (u32)v;
-      bad |= nc == 0xffffffffu ? 1u : 0u;
-      cnt_l[cc] = nc == 0xffffffffu ? 0u : nc;
-      below_max = max(below_max, (u32)(v >> 32));
+    for (int j = 0; j < J; ++j) {
+      u32 pos = joff[j] + ex[j];
+#pragma unroll
+      for (int e = 0; e < VL; ++e) {
+        const u32 kx = kz[j * VL + e];
+        if (kx >= tau) {
+          L.u.stage[pos] = ((u64)kx << 32) | (u32)ch.id(j, e);
+          ++pos;
+        }
+      }
     }
-    below_max = block_max(below_max, L.s);
-    bad = block_max(bad, L.s);
-    u32 why = bad ? kStOverflow : 0u;
-    bool done = false;
-    if (!why) {
-      u64 ent[kFPer];
-      const u32 tot = gather_lists(a, row_data(a, row), R, cnt_l, ent, L);
-      if (tot == 0xffffffffu)
-        why = kStOverflow;
-      else if (finish_topk(a, p, row, L, ent, tot, below_max))
-        done = true;
-      else
-        why = kStIncomplete;
+    lds_sync();
+    u64* reg = row_data(a, row) + (size_t)c * R;
+    for (u32 i = threadIdx.x; i < n; i += kThreads) {
+      const u64 st = L.u.stage[i];
+      const float q = qdiv(f_of_key((u32)(st >> 32)), p.T, p.rT, p.t_one);
+      stc(&reg[i], ((u64)skey(q) << 32) | (u32)st);
     }
-    if (!done) resolve_single<DT>(a, p, row, why, L);
-    reset_row(a, row);
-    return;
+    break;
   }
-
-  if (p.kind == kKindSingle) {
-    if (p.pen) lds_sync();
-    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
-    resolve_single<DT>(a, p, row, 0u, L);
-    reset_row(a, row);
-    return;
+  // largest z key left out
+  u32 below = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) below = kz[i] < tau ? max(below, kz[i]) : below;
+  below = block_max(below, L.s);
+  if (threadIdx.x == 0) stc(&sl[c].a, ((u64)below << 32) | n);
+  QS_TR(3);
+  if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return kNotLast;
+  QS_TR(4);
+  // ---- the row's last workgroup: gather and finish
+  u32* cnt_l = L.cties;
+  u32 below_max = 0, bad = 0;
+  for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
+    const u64 v = ldc(&sl[cc].a);
+    const u32 nc = (u32)v;
+    bad |= nc == 0xffffffffu ? 1u : 0u;
+    cnt_l[cc] = nc == 0xffffffffu ? 0u : nc;
+    below_max = max(below_max, (u32)(v >> 32));
   }
+  below_max = block_max(below_max, L.s);
+  bad = block_max(bad, L.s);
+  u32 why = bad ? kStOverflow : 0u;
+  bool done = false;
+  if (!why) {
+    u64 ent[kFPer];
+    const u32 tot = gather_lists(a, row_data(a, row), R, cnt_l, ent, L);
+    QS_TR(5);
+    if (tot == 0xffffffffu)
+      why = kStOverflow;
+    else if (finish_topk(a, p, row, L, ent, tot, below_max, c))
+      done = true;
+    else
+      why = kStIncomplete;
+  }
+  QS_TR(6);
+  return done ? 0u : why;
+}
 
-  // ---------------- mass rows (top-k off)
+// A top-k-off row: keys, the row barrier, weights, the bracket rounds, and (in
+// the row's last workgroup) the selection and the draw.  Returns as topk_row.
+template <int DT>
+__device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int row, const int c, Chunk<DT>& ch,
+                                        Lds& L) {
+  constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
+  RowSync* sy = &a.sync[row];
+  Slot* sl = row_slots(a, row);
   u32 kq[E];
   chunk_qkeys<DT>(ch, p, L, c, kq);
   if (p.pen) lds_sync();
@@ -1106,8 +1112,10 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
     kmn = ~block_max(~kmn, L.s);
     if (threadIdx.x == 0) stc(&sl[c].a, ((u64)kmx << 32) | kmn);
   }
+  QS_TR(2);
   (void)arrive(&sy->barA, L.s);
   bool ok = wait_count(a, row, &sy->barA, (u32)a.G, L.s);
+  QS_TR(3);
   u32 kstar = 0, kmin = 0xffffffffu;
   if (ok) {
     for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
@@ -1153,6 +1161,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
       stc(&sl[c].b, Sc);
       stc(&sl[c].c, (u64)nz);
     }
+    QS_TR(4);
     if (p.topp) {
       // Bracket the top-p boundary: each round histograms the tokens still in
       // the bracket into kNB bins linear in d, the last workgroup to arrive
@@ -1187,8 +1196,8 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
           // the reducer: bin totals, per-chunk maxima of the counts, the crossing bin
           u64 bm = 0;
           u32 bc = 0, bx = 0;
-          const int b = threadIdx.x;  // kNB == kThreads
-          int cc = 0;
+          const int b = threadIdx.x;  // bins 0..kNB-1, one per thread; threads past them hold zeros
+          int cc = b < kNB ? 0 : a.G;
           for (; cc + 8 <= a.G; cc += 8) {
             u64 vm[8];
             u32 vc[8];
@@ -1275,6 +1284,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
             sc = sc * (float)kNB;
           }
         }
+        QS_TR(5 + r);
       }
       if (ok) {
         // mass above the bracket, and the bracket's tokens listed in id order
@@ -1336,14 +1346,12 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
       }
     }
   }
-  if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+  QS_TR(8);
+  if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return kNotLast;
+  QS_TR(9);
   // ---- the row's last workgroup: the selector
   const u32 st = ldc(&sy->status);
-  if (st != 0u || kstar == 0u) {
-    resolve_single<DT>(a, p, row, st ? st : kStIncomplete, L);
-    reset_row(a, row);
-    return;
-  }
+  if (st != 0u || kstar == 0u) return st ? st : kStIncomplete;
   // per-chunk kept masses and tie counts in L.cmass / L.cties
   u64 W = 0, Tp = 0, A = 0, wt = 0;
   u32 klo = 1u, jties = 0xffffffffu, kept = 0, idlo = (u32)a.V;
@@ -1443,11 +1451,8 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
       }
     }
   }
-  if (!fine) {
-    resolve_single<DT>(a, p, row, kStList, L);
-    reset_row(a, row);
-    return;
-  }
+  QS_TR(10);
+  if (!fine) return kStList;
   if (!p.topp) {
     u64 tot = 0;
     for (int cc = 0; cc < a.G; ++cc) tot += L.cmass[cc];
@@ -1482,11 +1487,8 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
   const u64 tin = L.s.r64[13];
   const u32 jl = L.s.r[7];
   lds_sync();
-  if (owner < 0) {
-    resolve_single<DT>(a, p, row, kStIncomplete, L);
-    reset_row(a, row);
-    return;
-  }
+  if (owner < 0) return kStIncomplete;
+  QS_TR(11);
   // re-read the owner chunk and locate the token
   load_chunk<DT>(a, row, owner, ch);
   if (p.pen) pen_build(p, owner, L);
@@ -1500,12 +1502,66 @@ __global__ __launch_bounds__(kThreads) void k_sample(Args a) {
     return KW{above ? w : 0ull, ties_on && w && kq[i] == klo};
   };
   const int pick = chunk_locate<DT>(ch, kw, wt, jl, tin, L);
-  if (pick < 0) {
-    resolve_single<DT>(a, p, row, kStIncomplete, L);
-  } else {
-    write_result(a, row, p, pick, W, thr, p.topp ? kPathMassTopP : kPathMassAll, 0u, kstar, p.topp ? klo : 1u,
-                 p.topp ? idlo : (u32)a.V, kept);
+  if (pick < 0) return kStIncomplete;
+  write_result(a, row, p, pick, W, thr, p.topp ? kPathMassTopP : kPathMassAll, 0u, kstar, p.topp ? klo : 1u,
+               p.topp ? idlo : (u32)a.V, kept);
+  QS_TR(12);
+  return 0u;
+}
+
+// 128 VGPRs at most: two 512-thread workgroups per CU.
+template <int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_sample(Args a) {
+  __shared__ Lds L;
+  constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
+  const int c = blockIdx.x;
+  const int row = a.order ? gld(a.order + blockIdx.y) : (int)blockIdx.y;
+  if ((unsigned)row >= (unsigned)a.B) return;  // row_order must be a permutation of [0, B)
+  QS_TR(0);
+  Chunk<DT> ch;
+  load_chunk<DT>(a, row, c, ch);
+  const RowP p = row_params(a, row);
+  RowSync* sy = &a.sync[row];
+  Slot* sl = row_slots(a, row);
+  if (p.pen) pen_build(p, c, L);
+  QS_TR(1);
+  (void)E;
+  (void)J;
+  (void)VL;
+
+  if (p.kind == kKindGreedy) {
+    u64 best = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < VL; ++e) {
+        const float z = elem_z(ch, p, L, c, j, e);
+        const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+        best = pk > best ? pk : best;
+      }
+    if (p.pen) lds_sync();
+    best = block_max64(best, L.s);
+    if (threadIdx.x == 0) stc(&sl[c].a, best);
+    QS_TR(2);
+    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+    QS_TR(3);
+    finish_greedy(a, p, row, L);
+    reset_row(a, row);
+    QS_TR(4);
+    return;
   }
+
+  u32 why;
+  if (p.kind == kKindTopK) {
+    why = topk_row<DT>(a, p, row, c, ch, L);
+  } else if (p.kind == kKindSingle) {
+    if (p.pen) lds_sync();
+    why = arrive(&sy->arrive, L.s) == (u32)a.G - 1u ? kWhyLargeK : kNotLast;
+  } else {
+    why = mass_row<DT>(a, p, row, c, ch, L);
+  }
+  if (why == kNotLast) return;
+  if (why != 0u) resolve_single<DT>(a, row, why, L);
   reset_row(a, row);
 }
 
@@ -1519,14 +1575,20 @@ __global__ __launch_bounds__(kThreads) void k_probs(Args a) {
   Chunk<DT> ch;
   load_chunk<DT>(a, row, c, ch);
   const RowP p = row_params(a, row);
-  const RowRes r = a.res[row];
+  RowRes r;
+  r.id = gld(&a.res[row].id);
+  r.W = gld(&a.res[row].W);
+  r.thr = gld(&a.res[row].thr);
+  r.kstar = gld(&a.res[row].kstar);
+  r.klo = gld(&a.res[row].klo);
+  r.idlo = gld(&a.res[row].idlo);
   float* out = a.out_probs + (size_t)row * a.V;
   if (p.kind == kKindGreedy) {
 #pragma unroll
     for (int j = 0; j < Chunk<DT>::J; ++j)
 #pragma unroll
       for (int e = 0; e < Chunk<DT>::VL; ++e)
-        if (ch.valid(j, e)) out[ch.id(j, e)] = ch.id(j, e) == (int)r.id ? 1.0f : 0.0f;
+        if (ch.valid(j, e)) gst(out + ch.id(j, e), ch.id(j, e) == (int)r.id ? 1.0f : 0.0f);
     return;
   }
   if (p.pen) pen_build(p, c, L);
@@ -1544,12 +1606,12 @@ __global__ __launch_bounds__(kThreads) void k_probs(Args a) {
       u64 w = r.kstar ? weight_of(f_of_key(kq[i]), kq[i], qs, r.kstar, a.SH) : 0ull;
       w = w >= r.thr ? w : 0ull;
       const bool kept = kq[i] > r.klo || (kq[i] == r.klo && (u32)id <= r.idlo);
-      out[id] = (kept && w && r.W) ? (float)((double)w / Wd) : 0.0f;
+      gst(out + id, (kept && w && r.W) ? (float)((double)w / Wd) : 0.0f);
     }
 }
 
 __global__ void k_zero(u32* p, size_t n) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) gst(p + i, 0u);
 }
 
 }  // namespace qs

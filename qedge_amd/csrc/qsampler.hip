@@ -19,6 +19,9 @@ namespace {
 using namespace qs;
 
 thread_local char g_err[512] = "";
+#ifdef QS_TRACE
+void* g_trace = nullptr;
+#endif
 
 int fail(const char* fmt, long long v = 0) {
   snprintf(g_err, sizeof(g_err), fmt, v);
@@ -86,6 +89,11 @@ int max_rows_of(size_t bytes, int V) {
 extern "C" {
 
 int qs_version(void) { return 20000; }
+
+#ifdef QS_TRACE
+// Trace builds: [B, G, 16] u64 phase time stamps (device clock, 100 MHz) of the next calls.
+void qs_trace_buffer(void* p) { g_trace = p; }
+#endif
 
 const char* qs_last_error(void) { return g_err; }
 
@@ -166,6 +174,9 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   a.slots = (Slot*)(ws + LM.off_slots);
   a.data = (u64*)(ws + LM.off_data);
   a.data_per_row = LM.dpr;
+#ifdef QS_TRACE
+  a.trace = (u64*)g_trace;
+#endif
   const dim3 grid(L.G, B), block(kThreads);
   if (logits_dtype == QS_DTYPE_F32)
     hipLaunchKernelGGL(k_sample<QS_DTYPE_F32>, grid, block, 0, stream, a);
