@@ -30,8 +30,9 @@ constexpr int kWaveSpan = kCH / kWaves;    // contiguous ids per wave
 constexpr int kMaxG = 256;                 // chunks per row
 constexpr int kRegionTotal = 8192;         // top-k candidate entries per row (G * R)
 constexpr int kTopkMax = QS_TOPK_FAST_MAX; // top-k served from candidates
-constexpr int kFPer = 4096 / kThreads;     // gathered entries per finishing thread
-constexpr int kFCap = kFPer * kThreads;    // gathered entries per row
+constexpr int kFCap = 4096;                // gathered entries per row
+constexpr int kFPer = kFCap / kThreads;    // of them per finishing thread
+constexpr int kDirect = kThreads / 8;      // a selection bin this small is resolved by direct ranking
 constexpr int kNB = 256;                   // mass histogram bins (one per thread)
 constexpr int kRounds = 3;                 // bracket rounds before the exact path
 constexpr int kLC = 128;                   // bracket entries per chunk
@@ -98,17 +99,27 @@ struct Args {
   Slot* slots;  // [B, kMaxG]
   u64* data;    // [B, data_per_row]
   long long data_per_row;  // u64 entries
-  u64* trace;   // trace builds only: [B, G, 16] phase time stamps
+  u64* trace;   // trace builds only: [B, G, 32] phase time stamps
 };
 
 #ifdef QS_TRACE
 #define QS_TR(i)                                                                             \
   do {                                                                                       \
-    if (a.trace && threadIdx.x == 0) a.trace[((size_t)row * a.G + c) * 16 + (i)] = wall_clock64(); \
+    if (a.trace && threadIdx.x == 0) a.trace[((size_t)row * a.G + c) * 32 + (i)] = wall_clock64(); \
+  } while (0)
+// the same from code that has the arguments but not the row (slot of dispatch position blockIdx.y)
+#define QS_TRA(i)                                                                                     \
+  do {                                                                                                \
+    if (a.trace && threadIdx.x == 0) {                                                                \
+      a.trace[((size_t)blockIdx.y * a.G + blockIdx.x) * 32 + (i)] = wall_clock64();                  \
+    }                                                                                                 \
   } while (0)
 #else
 #define QS_TR(i) \
   do {           \
+  } while (0)
+#define QS_TRA(i) \
+  do {            \
   } while (0)
 #endif
 
@@ -150,14 +161,20 @@ struct SelLds {
   u32 hc[kNBS];
   u64 hm[kNBS];
 };
+struct FinLds {
+  u64 ent[kFCap];           // gathered entries (key << 32 | id), in id order
+  u32 lk[kDirect];          // a bin's keys for the direct resolution
+  u64 lw[kDirect];          // and their weights
+};
 struct Lds {
   union {
     u32 pen[kCH / 2];       // history counts of the chunk, two 16-bit counts per word
-    u64 mh[kNB];            // mass histogram of the chunk
+    u32 kq[kCH];            // top-k-off rows: keys of q, element i of thread t at i * kThreads + t
     u64 stage[kStageCap];   // entries staged for a region
+    FinLds fin;             // the finishing workgroup's candidates
   } u;
   SelLds sel;               // select histogram (beside the table: the exact pass needs both)
-  u32 hc[kNB];              // counts of the mass histogram
+  u64 mh[kNB];              // mass histogram of the chunk
   u64 cmass[kMaxG];         // finisher: per-chunk masses
   u32 cties[kMaxG];         // finisher: per-chunk tie counts
   u32 coff[kMaxG + 1];      // finisher: gathered offsets per chunk
@@ -747,193 +764,474 @@ __device__ __forceinline__ void finish_greedy(const Args& a, const RowP& p, int 
   write_result(a, row, p, (long long)id, 0, 0, kPathGreedy, 0u, 0u, 0u, id, 1u);
 }
 
-// Gather the entries of per-chunk lists (counts n_c, entries at base + c*stride)
-// in chunk order into registers: thread t holds positions [t*kFPer, (t+1)*kFPer).
-// Returns the total (or 0xffffffff when it exceeds kFCap).
-__device__ __forceinline__ u32 gather_lists(const Args& a, const u64* base, int stride, const u32* counts_lds,
-                                            u64 (&ent)[kFPer], Lds& L) {
-  // offsets
-  if (threadIdx.x < 64) {
-    u32 run = 0;
-    for (int c0 = 0; c0 < a.G; c0 += 64) {
-      const int c = c0 + (int)lane_id();
-      const u32 n = c < a.G ? counts_lds[c] : 0u;
-      const u32 inc = wave_incl_scan(n);
-      if (c < a.G) L.coff[c] = run + inc - n;
-      run += readlane(inc, 63);
-    }
-    if (lane_id() == 0) L.coff[a.G] = run;
+// ---------------------------------------------------------------- gathering candidates
+//
+// Entries of per-chunk lists (chunk c: cnt_of(c, mx) entries at base + c*stride,
+// in id order) go to L.u.fin.ent in chunk order, so the result is in id order.
+// The first P entries of every list (P a power of two) are loaded together with
+// the counts (one round trip); longer lists load the rest afterwards.
+// cnt_of(c, mx) returns 0xffffffff for a list that overflowed, and may set three
+// values mx[] whose workgroup maxima are returned in mx (threads past the lists
+// hold zeros).  Returns the total, or 0xffffffff when a list overflowed or the
+// total exceeds kFCap.  Needs G <= kThreads.
+template <typename CF>
+__device__ __forceinline__ u32 gather_lds(const Args& a, const u64* base, int stride, CF&& cnt_of, Lds& L,
+                                          u32 (&mx)[3]) {
+  constexpr int M = kFCap / kThreads;
+  const int G = a.G;
+  const int lp = 31 - __clz(min(stride, kFCap / G));
+  const int P = 1 << lp;
+  mx[0] = mx[1] = mx[2] = 0u;
+  const u32 raw = (int)threadIdx.x < G ? cnt_of((int)threadIdx.x, mx) : 0u;
+  u64 spec[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int f = (int)threadIdx.x + m * kThreads;
+    const int c = f >> lp, i = f & (P - 1);
+    spec[m] = c < G ? ldc(base + (size_t)c * stride + i) : 0ull;
+  }
+  const u32 nc = raw == 0xffffffffu ? (u32)kFCap + 1u : min(raw, (u32)kFCap + 1u);
+  // offsets (bit 24 counts the lists longer than P; the counts sum to less than
+  // 2^24) and the maxima, with one pair of barriers
+  const u32 v = nc | (nc > (u32)P ? 1u << 24 : 0u);
+  const u32 inc = wave_incl_scan(v);
+  const u32 m0 = wave_max(mx[0]), m1 = wave_max(mx[1]), m2 = wave_max(mx[2]);
+  if (lane_id() == 63) {
+    L.s.v[wave_id()][2] = inc;
+    L.s.v[wave_id()][5] = m0;
+    L.s.v[wave_id()][6] = m1;
+    L.s.v[wave_id()][7] = m2;
   }
   lds_sync();
-  const u32 total = L.coff[a.G];
+  u32 base_w = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const u32 x = L.s.v[i][2];
+    base_w += i < wave_id() ? x : 0u;
+    total += x;
+    mx[0] = max(mx[0], L.s.v[i][5]);
+    mx[1] = max(mx[1], L.s.v[i][6]);
+    mx[2] = max(mx[2], L.s.v[i][7]);
+  }
+  const u32 off = (base_w + inc - v) & 0xffffffu;
+  const bool any_long = (total >> 24) != 0u;
+  total &= 0xffffffu;
+  if ((int)threadIdx.x < G) {
+    L.coff[threadIdx.x] = off;
+    L.cties[threadIdx.x] = nc;
+  }
+  lds_sync();
   if (total > (u32)kFCap) return 0xffffffffu;
-  // thread t: positions f = t*kFPer + i; chunk of the first by binary search,
-  // then the offsets of all its entries, then every load at once
-  const u32 f0 = threadIdx.x * kFPer;
-  int c = 0;
-  {
-    int lo = 0, hi = a.G - 1;  // last c with coff[c] <= f0
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (L.coff[mid] <= f0) lo = mid; else hi = mid - 1;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int f = (int)threadIdx.x + m * kThreads;
+    const int c = f >> lp, i = f & (P - 1);
+    if (c < G && (u32)i < L.cties[c]) L.u.fin.ent[L.coff[c] + i] = spec[m];
+  }
+  if (any_long) {
+    for (int c = 0; c < G; ++c) {  // lists longer than P
+      const u32 n_c = L.cties[c];
+      for (u32 i = (u32)P + threadIdx.x; i < n_c; i += kThreads)
+        L.u.fin.ent[L.coff[c] + i] = ldc(base + (size_t)c * stride + i);
     }
-    c = lo;
   }
-  u32 off[kFPer];
-#pragma unroll
-  for (int i = 0; i < kFPer; ++i) {
-    const u32 f = f0 + i;
-    while (c < a.G - 1 && L.coff[c + 1] <= f) ++c;
-    off[i] = f < total ? (u32)c * (u32)stride + (f - L.coff[c]) : 0xffffffffu;
-  }
-#pragma unroll
-  for (int i = 0; i < kFPer; ++i) ent[i] = off[i] != 0xffffffffu ? ldc(base + off[i]) : 0ull;
+  lds_sync();
   return total;
 }
 
-// Finish from gathered entries (key << 32 | id) in id order, thread-contiguous:
-// select kappa_k (count k) when kk_on, weights, min_p, S, kappa_p (when top-p),
-// ties, the draw.  Returns false when the row must go to resolve_single.
-// For mass rows with top-p the entries are the boundary bin's tokens, A0 the
-// mass above it and Tp the row's target; per-chunk masses above the bin come in
-// L.cmass (already loaded) and the draw target is located to a chunk.
-__device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int row, Lds& L, u64 (&ent)[kFPer], u32 n,
-                                            u32 below_max, int c) {
-  const int SH = a.SH;
-  const u64 thr = ceil_scaled(p.mp, 23 + SH);
-  // key range of the candidates
-  u32 kmax = 0, kmin = 0xffffffffu;
+// ---------------------------------------------------------------- selection over the gathered entries
+
+// The gathered entries spread over the workgroup: thread t holds entries
+// [t*per, t*per + per) of L.u.fin.ent, per = ceil(n / kThreads) (<= kFPer),
+// so the thread order is the id order.  Missing entries are 0 (key 0).
+struct Held {
+  u64 e[kFPer];
+  u32 per;  // uniform
+};
+__device__ __forceinline__ void hold_entries(const Lds& L, u32 n, Held& h) {
+  h.per = uni((n + kThreads - 1) / kThreads);
+  const u32 i0 = threadIdx.x * h.per;
 #pragma unroll
   for (int i = 0; i < kFPer; ++i) {
-    const u32 key = (u32)(ent[i] >> 32);
-    if (threadIdx.x * kFPer + i < n) {
-      kmax = max(kmax, key);
-      kmin = min(kmin, key);
+    h.e[i] = 0ull;
+    if ((u32)i < h.per) h.e[i] = i0 + i < n ? L.u.fin.ent[i0 + i] : 0ull;
+  }
+}
+
+// floor(x / d) for a quotient below 2^20 (a float estimate, corrected).
+__device__ __forceinline__ u64 div_small(u64 x, u64 d) {
+  u64 q = (u64)fmaxf(0.0f, __builtin_floorf((float)x / (float)d));
+#pragma unroll
+  for (int i = 0; i < 2; ++i) q = q * d > x ? q - 1 : q;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) q = (q + 1) * d <= x ? q + 1 : q;
+  return q;
+}
+
+// Among the held entries whose key lies in [lo, hi] (by mass: whose packed
+// weight wq is nonzero) finds the key kappa at which the running total in
+// key-descending order crosses target:
+//   by count: count(key > kappa) < target <= count(key >= kappa)
+//   by mass:  mass(key > kappa) <= target < mass(key >= kappa).
+// Each round histograms the range into 256 bins of 2^s keys (one wave scans
+// them) and narrows to the crossing bin; a bin of at most kDirect entries is
+// resolved by ranking its entries directly; a bin of one key ends it.
+struct SelRes {
+  u32 kappa, cnt_above, cnt_at;
+  u64 mass_above, mass_at;
+  bool ok;
+};
+template <bool BY_MASS>
+__device__ __forceinline__ SelRes held_select(const Args& a, Lds& L, const Held& h, const u32 (&wq)[kFPer], u32 lo,
+                                              u32 hi, u64 target) {
+  (void)a;
+  SelRes r;
+  r.kappa = r.cnt_above = r.cnt_at = 0u;
+  r.mass_above = r.mass_at = 0ull;
+  r.ok = false;
+  for (int round = 0; round < 6; ++round) {
+    const int bl = bitlen(hi - lo);
+    const int sh = bl > 8 ? bl - 8 : 0;
+    if (round < 4) QS_TRA(15 + 3 * round);
+    for (int b = threadIdx.x; b < 256; b += kThreads) {
+      L.sel.hc[b] = 0u;
+      L.sel.hm[b] = 0ull;
+    }
+    lds_sync();
+#pragma unroll
+    for (int i = 0; i < kFPer; ++i) {
+      if ((u32)i < h.per) {
+        const u32 key = (u32)(h.e[i] >> 32);
+        if (key >= lo && key <= hi && (!BY_MASS || wq[i] != 0u)) {
+          const u32 b = (hi - key) >> sh;
+          atomicAdd(&L.sel.hc[b], 1u);
+          if (BY_MASS) atomicAdd(&L.sel.hm[b], wunpack(wq[i]));
+        }
+      }
+    }
+    lds_sync();
+    if (round < 4) QS_TRA(16 + 3 * round);
+    if (threadIdx.x < 64) {
+      const int l = (int)lane_id();
+      u32 c4[4], cs = 0;
+      u64 m4[4], ms = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c4[j] = L.sel.hc[4 * l + j];
+        m4[j] = BY_MASS ? L.sel.hm[4 * l + j] : 0ull;
+        cs += c4[j];
+        ms += m4[j];
+      }
+      const u32 ci = wave_incl_scan(cs);
+      const u64 mi = BY_MASS ? wave_incl_scan64(ms) : 0ull;
+      u32 cb = ci - cs;
+      u64 mb = mi - ms;
+      if (l == 0) L.s.r[4] = 0xffffffffu;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool hit = BY_MASS ? (mb <= target && target < mb + m4[j]) : (cb < target && target <= cb + c4[j]);
+        if (hit) {
+          L.s.r[4] = (u32)(4 * l + j);
+          L.s.r[5] = cb;
+          L.s.r[6] = c4[j];
+          L.s.r64[4] = mb;
+          L.s.r64[5] = m4[j];
+        }
+        cb += c4[j];
+        mb += m4[j];
+      }
+    }
+    lds_sync();
+    if (round < 4) QS_TRA(17 + 3 * round);
+    const u32 b = uni(L.s.r[4]);
+    const u32 cb = uni(L.s.r[5]), cnt_b = uni(L.s.r[6]);
+    const u64 mb = uni64(L.s.r64[4]), mass_b = uni64(L.s.r64[5]);
+    if (b == 0xffffffffu) {  // the target lies beyond the range's total
+      lds_sync();
+      return r;
+    }
+    r.cnt_above += cb;
+    r.mass_above += mb;
+    target -= BY_MASS ? mb : (u64)cb;
+    const u32 nhi = hi - (b << sh);
+    const u32 span = (1u << sh) - 1u;
+    const u32 nlo = (nhi - lo) > span ? nhi - span : lo;
+    if (sh == 0) {
+      r.kappa = nhi;
+      r.cnt_at = cnt_b;
+      r.mass_at = mass_b;
+      r.ok = true;
+      lds_sync();
+      return r;
+    }
+    hi = nhi;
+    lo = nlo;
+    if (cnt_b <= (u32)kDirect) {
+      // the bin's entries, ranked directly: entry x by the 8 threads 8x..8x+7
+      if (threadIdx.x == 0) {
+        L.s.r[7] = 0u;
+        L.s.r[8] = 0xffffffffu;
+      }
+      lds_sync();
+#pragma unroll
+      for (int i = 0; i < kFPer; ++i) {
+        if ((u32)i < h.per) {
+          const u32 key = (u32)(h.e[i] >> 32);
+          if (key >= lo && key <= hi && (!BY_MASS || wq[i] != 0u)) {
+            const u32 slot = atomicAdd(&L.s.r[7], 1u);
+            L.u.fin.lk[slot] = key;
+            L.u.fin.lw[slot] = BY_MASS ? wunpack(wq[i]) : 0ull;
+          }
+        }
+      }
+      lds_sync();
+      if (round < 4) QS_TRA(27);
+      const u32 m = uni(L.s.r[7]);
+      const u32 xi = threadIdx.x >> 3, part = threadIdx.x & 7u;
+      const u32 x = xi < m ? L.u.fin.lk[xi] : 0u;
+      u32 gc = 0, ec = 0;
+      u64 gm = 0, em = 0;
+      for (u32 j = part; j < m; j += 8) {
+        const u32 y = L.u.fin.lk[j];
+        const u64 wy = BY_MASS ? L.u.fin.lw[j] : 0ull;
+        gc += y > x ? 1u : 0u;
+        ec += y == x ? 1u : 0u;
+        gm += y > x ? wy : 0ull;
+        em += y == x ? wy : 0ull;
+      }
+#pragma unroll
+      for (int sh8 = 1; sh8 < 8; sh8 <<= 1) {
+        gc += __shfl_xor(gc, sh8);
+        ec += __shfl_xor(ec, sh8);
+        if (BY_MASS) {
+          gm += (u64)__shfl_xor((unsigned long long)gm, sh8);
+          em += (u64)__shfl_xor((unsigned long long)em, sh8);
+        }
+      }
+      if (xi < m && part == 0u) {
+        const bool hit = BY_MASS ? (gm <= target && target < gm + em) : (gc < target && target <= gc + ec);
+        if (hit) {
+          L.s.r[8] = x;
+          L.s.r[9] = gc;
+          L.s.r[10] = ec;
+          L.s.r64[6] = gm;
+          L.s.r64[7] = em;
+        }
+      }
+      lds_sync();
+      if (round < 4) QS_TRA(28);
+      const u32 kx = uni(L.s.r[8]);
+      r.kappa = kx;
+      r.cnt_above += uni(L.s.r[9]);
+      r.cnt_at = uni(L.s.r[10]);
+      r.mass_above += uni64(L.s.r64[6]);
+      r.mass_at = uni64(L.s.r64[7]);
+      r.ok = kx != 0xffffffffu;
+      lds_sync();
+      return r;
     }
   }
-  kmax = block_max(kmax, L.s);
-  kmin = ~block_max(~kmin, L.s);
-  QS_TR(7);
+  return r;
+}
+
+// Maxima of two values over the workgroup with one pair of barriers.
+__device__ __forceinline__ void block_max2(u32& x, u32& y, Scratch& s) {
+  x = wave_max(x);
+  y = wave_max(y);
+  if (lane_id() == 0) {
+    s.v[wave_id()][5] = x;
+    s.v[wave_id()][6] = y;
+  }
+  lds_sync();
+  x = y = 0u;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    x = max(x, s.v[i][5]);
+    y = max(y, s.v[i][6]);
+  }
+  lds_sync();
+}
+// Sums of a u64 and a u32 over the workgroup with one pair of barriers.
+__device__ __forceinline__ void block_sum2(u64& m, u32& c, Scratch& s) {
+  u32 ct;
+  u64 mt;
+  block_excl2(c, m, s, &ct, &mt);
+  c = ct;
+  m = mt;
+}
+
+// Finish a top-k row from its gathered candidates (L.u.fin.ent[0, n), id
+// order): kappa_k (count select), weights and min_p, S, kappa_p (mass select),
+// the draw by an id-order scan.  kmax is the row's largest key of q, klow a
+// lower bound of the candidates' keys, below_max the largest z key left out by
+// any chunk.  Returns false when the row must go to the exact path.
+__device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int row, Lds& L, u32 n, u32 kmax, u32 klow,
+                                            u32 below_max, int c) {
+  (void)c;
+  const int SH = a.SH;
+  const u64 thr = ceil_scaled(p.mp, 23 + SH);
   if (n == 0 || kmax == 0u) return false;
+  const float qs = f_of_key(kmax);
+  auto wpk = [&](u32 key) -> u32 {
+    const u32 x = wpack_of(f_of_key(key), key, qs, kmax, SH);
+    return wunpack(x) >= thr ? x : 0u;
+  };
+  auto wf = [&](u32 key) -> u64 { return wunpack(wpk(key)); };
+  Held h;
+  hold_entries(L, n, h);
+  u32 wq[kFPer];
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i) wq[i] = 0u;
+  QS_TR(9);
   // kappa_k
   u32 kk;
   if (n < (u32)p.k) {
     if (below_max != 0u) return false;  // tokens left out could belong to K
     kk = 1u;
   } else {
-    Sel q;
-    sel_init(q, kmin, kmax, false, (u64)p.k);
-    for (;;) {
-      sel_clear(L);
-      lds_sync();
-#pragma unroll
-      for (int i = 0; i < kFPer; ++i)
-        if (threadIdx.x * kFPer + i < n) sel_add(q, L, (u32)(ent[i] >> 32), 0);
-      lds_sync();
-      if (sel_step(q, L)) break;
-    }
-    if (q.found != 1) return false;
+    const SelRes q = held_select<false>(a, L, h, wq, max(klow, 1u), kmax, (u64)p.k);
+    if (!q.ok) return false;
     kk = q.kappa;
     // completeness: every token left out has a key of q below kappa_k
-    if (below_max != 0u) {
-      const float zb = f_of_key(below_max);
-      const u32 kb = skey(qdiv(zb, p.T, p.rT, p.t_one));
-      if (kb >= kk) return false;
-    }
+    if (below_max != 0u && skey(qdiv(f_of_key(below_max), p.T, p.rT, p.t_one)) >= kk) return false;
   }
-  QS_TR(8);
-  const float qs = f_of_key(kmax);
-  u32 wq[kFPer];  // packed weights
+  QS_TR(10);
+  // weights of K (packed), S and the count of nonzero weights
   u64 S = 0;
   u32 nz = 0;
 #pragma unroll
   for (int i = 0; i < kFPer; ++i) {
-    const u32 key = (u32)(ent[i] >> 32);
-    u32 x = (threadIdx.x * kFPer + i < n && key >= kk) ? wpack_of(f_of_key(key), key, qs, kmax, SH) : 0u;
-    const u64 wx = wunpack(x);
-    x = wx >= thr ? x : 0u;
-    wq[i] = x;
-    S += x ? wx : 0ull;
-    nz += x ? 1u : 0u;
+    if ((u32)i < h.per) {
+      const u32 key = (u32)(h.e[i] >> 32);
+      wq[i] = key >= kk ? wpk(key) : 0u;
+      S += wunpack(wq[i]);
+      nz += wq[i] ? 1u : 0u;
+    }
   }
-  S = block_sum64(S, L.s);
-  nz = block_sum(nz, L.s);
+  block_sum2(S, nz, L.s);
   u32 klo = kk, jties = 0xffffffffu, kept = nz;
   u64 W = S, wt = 0;
-  QS_TR(9);
+  QS_TR(11);
   if (p.topp) {
     const u64 Tp = mul_frac(S, p.tp);
-    Sel q;
-    sel_init(q, kk, kmax, true, Tp);
-    for (;;) {
-      sel_clear(L);
-      lds_sync();
-#pragma unroll
-      for (int i = 0; i < kFPer; ++i)
-        if (wq[i]) sel_add(q, L, (u32)(ent[i] >> 32), wunpack(wq[i]));
-      lds_sync();
-      if (sel_step(q, L)) break;
-    }
-    if (q.found != 1) return false;
+    const SelRes q = held_select<true>(a, L, h, wq, kk, kmax, Tp);
+    if (!q.ok) return false;
     klo = q.kappa;
-    wt = q.kmass / q.kcount;
-    const u64 A = q.above_m;
-    const u64 jj = (Tp - A) / wt + 1ull;
-    jties = (u32)(jj < (u64)q.kcount ? jj : (u64)q.kcount);
-    W = A + (u64)jties * wt;
-    kept = q.above_c + jties;
+    wt = wf(klo);  // every token at kappa_p has this weight
+    const u64 jj = div_small(Tp - q.mass_above, wt) + 1ull;
+    jties = (u32)(jj < (u64)q.cnt_at ? jj : (u64)q.cnt_at);
+    W = q.mass_above + (u64)jties * wt;
+    kept = q.cnt_above + jties;
   }
-  QS_TR(10);
-  // the draw over the entries in id order (thread-contiguous)
+  QS_TR(12);
+  // the draw: kept mass in id order, ties at klo counting wt each up to jties of them
+  const bool ties_on = jties != 0xffffffffu;
+  const u32 jt = ties_on ? jties : 0u;
   const u64 t = mul_frac(W, p.u);
   u64 m = 0;
   u32 tc = 0;
 #pragma unroll
   for (int i = 0; i < kFPer; ++i) {
-    const u32 key = (u32)(ent[i] >> 32);
-    const bool above = jties == 0xffffffffu ? (key >= klo) : (key > klo);
-    m += above ? wunpack(wq[i]) : 0ull;
-    tc += (jties != 0xffffffffu && wq[i] && key == klo) ? 1u : 0u;
+    if ((u32)i < h.per) {
+      const u32 key = (u32)(h.e[i] >> 32);
+      m += (ties_on ? key > klo : key >= klo) ? wunpack(wq[i]) : 0ull;
+      tc += (ties_on && wq[i] && key == klo) ? 1u : 0u;
+    }
   }
   u32 ttot;
   u64 mtot;
   block_excl2(tc, m, L.s, &ttot, &mtot);
   if (threadIdx.x == 0) {
-    L.s.r[10] = 0xffffffffu;
     L.s.r[11] = 0xffffffffu;
+    L.s.r[12] = 0xffffffffu;
   }
   lds_sync();
 #pragma unroll
   for (int i = 0; i < kFPer; ++i) {
-    const u32 key = (u32)(ent[i] >> 32);
-    const bool above = jties == 0xffffffffu ? (key >= klo) : (key > klo);
-    const bool tie = jties != 0xffffffffu && wq[i] && key == klo;
-    const u64 before = m + (u64)min(tc, jties == 0xffffffffu ? 0u : jties) * wt;
-    m += above ? wunpack(wq[i]) : 0ull;
-    tc += tie ? 1u : 0u;
-    const u64 after = m + (u64)min(tc, jties == 0xffffffffu ? 0u : jties) * wt;
-    if (before <= t && t < after) L.s.r[10] = (u32)ent[i];
-    if (tie && tc == jties) L.s.r[11] = (u32)ent[i];
+    if ((u32)i < h.per) {
+      const u32 key = (u32)(h.e[i] >> 32);
+      const bool tie = ties_on && wq[i] && key == klo;
+      const u64 before = m + (u64)min(tc, jt) * wt;
+      m += (ties_on ? key > klo : key >= klo) ? wunpack(wq[i]) : 0ull;
+      tc += tie ? 1u : 0u;
+      const u64 after = m + (u64)min(tc, jt) * wt;
+      if (before <= t && t < after) L.s.r[11] = (u32)h.e[i];
+      if (tie && tc == jties) L.s.r[12] = (u32)h.e[i];
+    }
   }
   lds_sync();
-  QS_TR(11);
-  const u32 pick = L.s.r[10];
-  const u32 idlo = jties == 0xffffffffu ? (u32)a.V : L.s.r[11];
+  QS_TR(13);
+  const u32 pick = L.s.r[11];
+  const u32 idlo = ties_on ? L.s.r[12] : (u32)a.V;
   if (pick == 0xffffffffu) return false;
   write_result(a, row, p, (long long)pick, W, thr, kPathTopK, 0u, kmax, klo, idlo, kept);
   return true;
 }
 
-// Bin of the mass histogram: linear in -d = q* - q past an offset d0 (bin 0
-// holds the largest keys), clamped to [0, kNB), monotone in the key.
-__device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, float d0, float scale) {
-  const float d = (k == ks) ? 0.0f : q - qs;
-  return min((u32)kNB - 1u, (u32)fmaxf(0.0f, (-d - d0) * scale));
+// Bins of the mass histogram over x = -d = q* - q past an offset x0: bins
+// [0, n1) linear with n1 / x1 bins per unit up to x0 + x1, bins [n1, kNB) linear
+// with s2 bins per unit past it; bin 0 holds the largest keys, everything past
+// the range falls in the last bin.  Monotone in the key.
+struct MassBins {
+  float x0, x1, s1, s2;
+  int n1;
+};
+constexpr float kXMax = 44.5f;  // y = -x * log2(e) < -64 past it: weight 0
+constexpr float kXFine = 12.0f; // first round: the finer segment, [0, kXFine)
+__device__ __forceinline__ MassBins mass_bins_first(float D) {
+  MassBins m;
+  m.x0 = 0.0f;
+  D = fminf(fmaxf(D, 0.0f), kXMax);
+  if (D > 16.0f) {
+    m.n1 = 3 * kNB / 4;
+    m.x1 = kXFine;
+    m.s1 = (float)m.n1 / kXFine;
+    m.s2 = (float)(kNB - m.n1) / (D - kXFine);
+  } else {
+    m.n1 = kNB;
+    m.x1 = D > 0x1p-60f ? D : 0.0f;
+    m.s1 = D > 0x1p-60f ? (float)kNB / D : 0.0f;  // no spread: every token in bin 0
+    m.s2 = 0.0f;
+  }
+  return m;
 }
-// Per-row data of top-k-off rows: bin masses [G][kNB] u64, bin counts [G][kNB]
-// u32, then the listed tokens [G][kLC].
+__device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, const MassBins& m) {
+  const float d = (k == ks) ? 0.0f : q - qs;
+  const float x = -d - m.x0;
+  const float f = x < m.x1 ? x * m.s1 : (float)m.n1 + (x - m.x1) * m.s2;
+  return min((u32)kNB - 1u, (u32)fmaxf(0.0f, f));
+}
+// x at the far edge of bin b
+__device__ __forceinline__ float bin_edge(const MassBins& m, u32 b) {
+  const float e = (float)(b + 1);
+  if ((int)b < m.n1) return m.x0 + (m.s1 > 0.0f ? e / m.s1 : 0.0f);
+  return m.x0 + m.x1 + (m.s2 > 0.0f ? (e - (float)m.n1) / m.s2 : 3.0e38f);
+}
+// A lower bound of the nonzero weights in bin b: 2^(23 + SH) * 2^(-edge * log2 e)
+// with room for the rounding of the bin computation, and never below 1 (every
+// nonzero weight is at least 1).  A token with nonzero weight has x < kXMax, so
+// the last bin of every range is bounded too.
+__device__ __forceinline__ float bin_least_weight(const MassBins& m, u32 b, int SH) {
+  const float xe = fminf(bin_edge(m, b) * 1.001f + 1e-6f, kXMax);
+  return fmaxf(1.0f, 0.9f * exp2f((float)(23 + SH) - xe * kL2E));
+}
+// The bins of the next round: bin b of this one split into kNB.
+__device__ __forceinline__ MassBins mass_bins_split(const MassBins& m, u32 b) {
+  const float lo = b == 0u ? m.x0 : bin_edge(m, b - 1u);
+  const float hi = bin_edge(m, b);
+  MassBins n;
+  n.x0 = lo;
+  n.n1 = kNB;
+  const float w = fminf(hi, kXMax) - lo;
+  n.x1 = w > 0.0f ? w : 0.0f;
+  n.s1 = w > 0x1p-60f ? (float)kNB / w : 0.0f;
+  n.s2 = 0.0f;
+  return n;
+}
+// Per-row data of top-k-off rows: bin masses [G][kNB] u64, then the listed
+// tokens [G][kLC].
 __device__ __forceinline__ u64* list_base(const Args& a, int row) {
-  return row_data(a, row) + (size_t)a.G * kNB + (size_t)a.G * kNB / 2;
+  return row_data(a, row) + (size_t)a.G * kNB;
 }
 
 // ---------------------------------------------------------------- the streaming kernel
@@ -959,6 +1257,7 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
       m = max(m, kx);
     }
   if (p.pen) lds_sync();
+  QS_TR(2);
   // quota of the chunk and of each wave
   const int vin = min(kCH, a.V - c * kCH);
   const int nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
@@ -966,21 +1265,41 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
   int kc = (int)ceilf(mu + 4.0f * sqrtf(mu) + 2.0f);
   kc = min(kc, p.k);
   const int kw = min(64, max(1, (kc + nw - 1) / nw));
-  // the kw-th largest per-thread maximum of the wave
+  // tw: the kw-th largest per-thread maximum of the wave, to the top 16 key bits
+  // (lanes holding a maximum >= tw: at least kw); tau: the jw-th largest tw over
+  // the waves, jw = ceil(kc / kw), so that jw waves hold kw tokens >= tau each
   u32 tw = 0;
-  for (int b = 31; b >= 0; --b) {
-    const u32 cand = tw | (1u << b);
-    if ((int)popc64(__ballot(m >= cand)) >= kw) tw = cand;
+  {
+    const u32 m16 = m >> 16;
+    for (int b = 15; b >= 0; --b) {
+      const u32 cand = tw | (1u << b);
+      if ((int)popc64(__ballot(m16 >= cand)) >= kw) tw = cand;
+    }
+    tw <<= 16;
   }
-  const bool wave_live = wave_id() < nw;
-  if (lane_id() == 0) L.s.v[wave_id()][4] = wave_live ? tw : 0xffffffffu;
+  if (lane_id() == 0) L.s.v[wave_id()][4] = wave_id() < nw ? tw : 0u;
   lds_sync();
-  u32 tau = 0xffffffffu;
+  const int jw = min(nw, (kc + kw - 1) / kw);
+  u32 tau;
+  {
+    u32 tv[kWaves];
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) tau = min(tau, L.s.v[i][4]);
+    for (int i = 0; i < kWaves; ++i) tv[i] = uni(L.s.v[i][4]);
+    static_assert(kWaves == 8, "sorting network for 8 waves");
+    constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3},
+                                {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+    for (int i = 0; i < 19; ++i) {
+      const u32 x = tv[net[i][0]], y = tv[net[i][1]];
+      tv[net[i][0]] = max(x, y);
+      tv[net[i][1]] = min(x, y);
+    }
+    tau = tv[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) tau = (i == jw - 1) ? tv[i] : tau;
+  }
   tau = max(tau, 1u);
-  lds_sync();
-  QS_TR(2);
+  QS_TR(3);
   const int R = a.R;
   u32 n = 0;
   for (int attempt = 0; attempt < 2; ++attempt) {
@@ -1050,43 +1369,44 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
       const float q = qdiv(f_of_key((u32)(st >> 32)), p.T, p.rT, p.t_one);
       stc(&reg[i], ((u64)skey(q) << 32) | (u32)st);
     }
+    QS_TR(4);
     break;
   }
-  // largest z key left out
-  u32 below = 0;
+  // largest z key left out, and the chunk's largest; the q keys of the latter and of tau
+  u32 below = 0, zmax = m;
 #pragma unroll
   for (int i = 0; i < E; ++i) below = kz[i] < tau ? max(below, kz[i]) : below;
-  below = block_max(below, L.s);
-  if (threadIdx.x == 0) stc(&sl[c].a, ((u64)below << 32) | n);
-  QS_TR(3);
+  block_max2(below, zmax, L.s);
+  if (threadIdx.x == 0) {
+    const u32 qmax = zmax ? skey(qdiv(f_of_key(zmax), p.T, p.rT, p.t_one)) : 0u;
+    const u32 qlow = skey(qdiv(f_of_key(tau), p.T, p.rT, p.t_one));
+    stc(&sl[c].a, ((u64)below << 32) | n);
+    stc(&sl[c].d, ((u64)qmax << 32) | qlow);
+  }
+  QS_TR(5);
   if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return kNotLast;
-  QS_TR(4);
-  // ---- the row's last workgroup: gather and finish
-  u32* cnt_l = L.cties;
-  u32 below_max = 0, bad = 0;
-  for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
-    const u64 v = ldc(&sl[cc].a);
-    const u32 nc = (u32)v;
-    bad |= nc == 0xffffffffu ? 1u : 0u;
-    cnt_l[cc] = nc == 0xffffffffu ? 0u : nc;
-    below_max = max(below_max, (u32)(v >> 32));
-  }
-  below_max = block_max(below_max, L.s);
-  bad = block_max(bad, L.s);
-  u32 why = bad ? kStOverflow : 0u;
-  bool done = false;
-  if (!why) {
-    u64 ent[kFPer];
-    const u32 tot = gather_lists(a, row_data(a, row), R, cnt_l, ent, L);
-    QS_TR(5);
-    if (tot == 0xffffffffu)
-      why = kStOverflow;
-    else if (finish_topk(a, p, row, L, ent, tot, below_max, c))
-      done = true;
-    else
-      why = kStIncomplete;
-  }
   QS_TR(6);
+  // ---- the row's last workgroup: gather and finish
+  u32 mx[3];
+  const u32 tot = gather_lds(a, row_data(a, row), R, [&](int cc, u32(&v)[3]) -> u32 {
+    const u64 x = ldc(&sl[cc].a), d = ldc(&sl[cc].d);
+    v[0] = (u32)(x >> 32);  // largest z key left out
+    v[1] = (u32)(d >> 32);  // largest q key
+    v[2] = ~(u32)d;         // the complement of the q key of the chunk's threshold
+    return (u32)x;
+  }, L, mx);
+  QS_TR(7);
+  const u32 below_max = mx[0], qmax = mx[1], qlow = ~mx[2];
+  QS_TR(8);
+  u32 why = 0u;
+  bool done = false;
+  if (tot == 0xffffffffu)
+    why = kStOverflow;
+  else if (finish_topk(a, p, row, L, tot, qmax, qlow, below_max, c))
+    done = true;
+  else
+    why = kStIncomplete;
+  QS_TR(14);
   return done ? 0u : why;
 }
 
@@ -1098,15 +1418,16 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
   RowSync* sy = &a.sync[row];
   Slot* sl = row_slots(a, row);
-  u32 kq[E];
-  chunk_qkeys<DT>(ch, p, L, c, kq);
-  if (p.pen) lds_sync();
   {
+    u32 kr[E];
+    chunk_qkeys<DT>(ch, p, L, c, kr);
+    if (p.pen) lds_sync();  // the count table is read no more: the keys go over it
     u32 kmx = 0, kmn = 0xffffffffu;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      kmx = max(kmx, kq[i]);
-      if (kq[i]) kmn = min(kmn, kq[i]);
+      kmx = max(kmx, kr[i]);
+      if (kr[i]) kmn = min(kmn, kr[i]);
+      L.u.kq[i * kThreads + threadIdx.x] = kr[i];
     }
     kmx = block_max(kmx, L.s);
     kmn = ~block_max(~kmn, L.s);
@@ -1125,6 +1446,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     }
     kstar = block_max(kstar, L.s);
     kmin = ~block_max(~kmin, L.s);
+    QS_TR(4);
     if (kstar == 0u) {
       fail_row(a, row, kStIncomplete);  // no weights: resolved alone
       ok = false;
@@ -1133,91 +1455,91 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   const int SH = a.SH;
   const u64 thr = ceil_scaled(p.mp, 23 + SH);
   const float qs = f_of_key(kstar);
-  // bins linear in d = q - q* over [max(q_min, q* - 44.5), q*]
-  float scale = 0.0f;
-  {
-    const float qmin = f_of_key(kmin);
-    const float span = qs - fmaxf(qmin, qs - 44.5f);
-    scale = span > 0x1p-60f ? (float)kNB / span : 0.0f;  // no spread: every token in bin 0
-  }
+  // first-round bins over x = q* - q in [0, D], D = min(q* - q_min, kXMax)
+  MassBins mb = mass_bins_first(qs - f_of_key(kmin));
   if (ok) {
-    // weights (packed, kept in registers) and the chunk's mass
+    // weights (packed, kept in registers), the chunk's mass and (top-p) the
+    // first-round mass histogram, in one pass
+    if (p.topp) {
+      for (int b = threadIdx.x; b < kNB; b += kThreads) L.mh[b] = 0ull;
+      lds_sync();
+    }
     u32 wp[E];
     u64 Sc = 0;
     u32 nz = 0, inb = 0;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      u32 x = wpack_of(f_of_key(kq[i]), kq[i], qs, kstar, SH);
+      const u32 k = L.u.kq[i * kThreads + threadIdx.x];
+      const float q = f_of_key(k);
+      u32 x = wpack_of(q, k, qs, kstar, SH);
       const u64 w = wunpack(x);
       x = w >= thr ? x : 0u;
       wp[i] = x;
       Sc += x ? w : 0ull;
       nz += x ? 1u : 0u;
       inb |= (x ? 1u : 0u) << i;
+      if (p.topp && x) atomicAdd(&L.mh[mass_bin(q, k, qs, kstar, mb)], w);
     }
-    Sc = block_sum64(Sc, L.s);
-    nz = block_sum(nz, L.s);
+    QS_TR(5);
+    block_sum2(Sc, nz, L.s);  // its barriers also complete the histogram
     if (threadIdx.x == 0) {
       stc(&sl[c].b, Sc);
       stc(&sl[c].c, (u64)nz);
     }
-    QS_TR(4);
+    QS_TR(6);
     if (p.topp) {
-      // Bracket the top-p boundary: each round histograms the tokens still in
-      // the bracket into kNB bins linear in d, the last workgroup to arrive
-      // (the reducer) picks the bin holding the boundary and either lists it
-      // (small enough) or has every workgroup split it again.
+      // Bracket the top-p boundary: each round's mass histogram of the tokens
+      // still in the bracket is published; the last workgroup to arrive (the
+      // reducer) picks the bin holding the boundary and either has it listed
+      // (few enough tokens, bounded by the bin's mass over its least weight)
+      // or has every workgroup split it again.
       u32 abv = 0;  // tokens above the bracket
-      float d0 = 0.0f, sc = scale;
       u64* hm_g = row_data(a, row);
-      u32* hc_g = (u32*)(row_data(a, row) + (size_t)a.G * kNB);
       bool listed = false;
       for (int r = 0; r < kRounds && ok && !listed; ++r) {
-        for (int b = threadIdx.x; b < kNB; b += kThreads) {
-          L.u.mh[b] = 0ull;
-          L.hc[b] = 0u;
-        }
-        lds_sync();
+        if (r > 0) {
+          for (int b = threadIdx.x; b < kNB; b += kThreads) L.mh[b] = 0ull;
+          lds_sync();
 #pragma unroll
-        for (int i = 0; i < E; ++i) {
-          if ((inb >> i) & 1u) {
-            const u32 b = mass_bin(f_of_key(kq[i]), kq[i], qs, kstar, d0, sc);
-            atomicAdd(&L.u.mh[b], wunpack(wp[i]));
-            atomicAdd(&L.hc[b], 1u);
+          for (int i = 0; i < E; ++i) {
+            if ((inb >> i) & 1u)
+              atomicAdd(&L.mh[mass_bin(f_of_key(L.u.kq[i * kThreads + threadIdx.x]), L.u.kq[i * kThreads + threadIdx.x], qs, kstar, mb)], wunpack(wp[i]));
           }
+          lds_sync();
         }
-        lds_sync();
-        for (int b = threadIdx.x; b < kNB; b += kThreads) {
-          stc(&hm_g[(size_t)c * kNB + b], L.u.mh[b]);
-          stc(&hc_g[(size_t)c * kNB + b], L.hc[b]);
-        }
+        QS_TR(7 + 4 * r);
+        for (int b = threadIdx.x; b < kNB; b += kThreads) stc(&hm_g[(size_t)c * kNB + b], L.mh[b]);
         const u32 before = arrive(&sy->barB, L.s);
+        QS_TR(8 + 4 * r);
         if (before == (u32)a.G * (u32)(r + 1) - 1u) {
-          // the reducer: bin totals, per-chunk maxima of the counts, the crossing bin
-          u64 bm = 0;
-          u32 bc = 0, bx = 0;
-          const int b = threadIdx.x;  // bins 0..kNB-1, one per thread; threads past them hold zeros
-          int cc = b < kNB ? 0 : a.G;
-          for (; cc + 8 <= a.G; cc += 8) {
-            u64 vm[8];
-            u32 vc[8];
+          // the reducer: per bin the total over the chunks and the largest
+          // chunk share (thread t: bin t % kNB, every second chunk from t / kNB)
+          static_assert(kThreads == 2 * kNB, "two threads per bin");
+          const int b = threadIdx.x & (kNB - 1), h = threadIdx.x / kNB;
+          u64 bm = 0, bx = 0;
+          for (int c0 = h; c0 < a.G; c0 += 16) {
+            u64 v[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              vm[i] = ldc(&hm_g[(size_t)(cc + i) * kNB + b]);
-              vc[i] = ldc(&hc_g[(size_t)(cc + i) * kNB + b]);
+            for (int j = 0; j < 8; ++j) {
+              const int cc = c0 + 2 * j;
+              v[j] = cc < a.G ? ldc(&hm_g[(size_t)cc * kNB + b]) : 0ull;
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              bm += vm[i];
-              bc += vc[i];
-              bx = max(bx, vc[i]);
+            for (int j = 0; j < 8; ++j) {
+              bm += v[j];
+              bx = v[j] > bx ? v[j] : bx;
             }
           }
-          for (; cc < a.G; ++cc) {
-            bm += ldc(&hm_g[(size_t)cc * kNB + b]);
-            const u32 v = ldc(&hc_g[(size_t)cc * kNB + b]);
-            bc += v;
-            bx = max(bx, v);
+          if (h == 1) {
+            L.sel.hm[b] = bm;
+            L.sel.hm[kNB + b] = bx;
+          }
+          lds_sync();
+          if (h == 0) {
+            bm += L.sel.hm[b];
+            bx = L.sel.hm[kNB + b] > bx ? L.sel.hm[kNB + b] : bx;
+          } else {
+            bm = bx = 0ull;
           }
           u64 tot;
           const u64 ex = block_excl64(bm, L.s, &tot);
@@ -1232,11 +1554,13 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
           const u64 target = Tp - A;
           if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
           lds_sync();
-          if (ex <= target && target < ex + bm) {
+          if (h == 0 && ex <= target && target < ex + bm) {
             L.s.r[12] = (u32)b;
             L.s.r64[12] = ex;
-            L.s.r[13] = bc;
-            L.s.r[14] = bx;
+            // tokens of the bin: at most its mass over its least weight
+            const float wl = bin_least_weight(mb, b, SH);
+            const float nb = wl > 0.0f ? (float)bm / wl : 3.0e38f, nx = wl > 0.0f ? (float)bx / wl : 3.0e38f;
+            L.s.r[13] = (nb <= (float)kFCap && nx <= (float)kLC) ? 1u : 0u;
           }
           lds_sync();
           const u32 bsel = L.s.r[12];
@@ -1246,8 +1570,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
             if (bsel == 0xffffffffu) {
               act = 2;
             } else {
-              const bool small = L.s.r[13] <= (u32)kFCap && L.s.r[14] <= (u32)kLC;
-              act = small ? 1u : (r + 1 < kRounds ? 0u : 2u);
+              act = L.s.r[13] ? 1u : (r + 1 < kRounds ? 0u : 2u);
               if (r == 0) {
                 stc(&rr->Tp, Tp);
                 stc(&rr->S, tot);
@@ -1262,6 +1585,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
         } else {
           ok = wait_count(a, row, &sy->dec, (u32)(r + 1) << 16, L.s);
         }
+        QS_TR(9 + 4 * r);
         if (ok) {
           if (threadIdx.x == 0) L.s.r[15] = ldc(&sy->dec);
           lds_sync();
@@ -1274,17 +1598,16 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
 #pragma unroll
             for (int i = 0; i < E; ++i) {
               if ((inb >> i) & 1u) {
-                const u32 b = mass_bin(f_of_key(kq[i]), kq[i], qs, kstar, d0, sc);
+                const u32 b = mass_bin(f_of_key(L.u.kq[i * kThreads + threadIdx.x]), L.u.kq[i * kThreads + threadIdx.x], qs, kstar, mb);
                 if (b < bsel) abv |= 1u << i;
                 if (b != bsel) inb &= ~(1u << i);
               }
             }
             listed = act == 1u;
-            d0 = d0 + (float)bsel / sc;
-            sc = sc * (float)kNB;
+            mb = mass_bins_split(mb, bsel);
           }
         }
-        QS_TR(5 + r);
+        QS_TR(10 + 4 * r);
       }
       if (ok) {
         // mass above the bracket, and the bracket's tokens listed in id order
@@ -1297,8 +1620,8 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
           above += ((abv >> i) & 1u) ? wunpack(wp[i]) : 0ull;
           cnt[i / VL] += (inb >> i) & 1u;
         }
-        above = block_sum64(above, L.s);
-        const u32 na = block_sum((u32)__popc(abv), L.s);
+        u32 na = (u32)__popc(abv);
+        block_sum2(above, na, L.s);
         u32 ex[J], tot = 0;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
@@ -1334,21 +1657,22 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
           for (int e = 0; e < VL; ++e) {
             const int i = j * VL + e;
             if ((inb >> i) & 1u) {
-              stc(&lst[pos], ((u64)kq[i] << 32) | (u32)ch.id(j, e));
+              if (pos < (u32)kLC) stc(&lst[pos], ((u64)L.u.kq[i * kThreads + threadIdx.x] << 32) | (u32)ch.id(j, e));
               ++pos;
             }
           }
         }
         if (threadIdx.x == 0) {
+          if (nl > (u32)kLC) orc(&sy->status, kStOverflow);  // more than the bound allowed for
           stc(&sl[c].b, above);
           stc(&sl[c].c, ((u64)nl << 32) | na);
         }
       }
     }
   }
-  QS_TR(8);
+  QS_TR(19);
   if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return kNotLast;
-  QS_TR(9);
+  QS_TR(20);
   // ---- the row's last workgroup: the selector
   const u32 st = ldc(&sy->status);
   if (st != 0u || kstar == 0u) return st ? st : kStIncomplete;
@@ -1356,6 +1680,11 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   u64 W = 0, Tp = 0, A = 0, wt = 0;
   u32 klo = 1u, jties = 0xffffffffu, kept = 0, idlo = (u32)a.V;
   bool fine = true;
+  auto wpk = [&](u32 key) -> u32 {
+    const u32 x = wpack_of(f_of_key(key), key, qs, kstar, SH);
+    return wunpack(x) >= thr ? x : 0u;
+  };
+  auto wf = [&](u32 key) -> u64 { return wunpack(wpk(key)); };
   if (!p.topp) {
     u32 nzt = 0;
     for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
@@ -1368,82 +1697,75 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     Tp = ldc(&a.res[row].Tp);
     const u64 Ahi = ldc(&a.res[row].Ahi);
     u32 nat = 0;
-    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
+    u32 mx[3];
+    const u32 n = gather_lds(a, list_base(a, row), kLC, [&](int cc, u32(&)[3]) -> u32 {
       const u64 cv = ldc(&sl[cc].c);
       L.cmass[cc] = ldc(&sl[cc].b);
-      L.coff[cc] = 0;
-      L.cties[cc] = (u32)(cv >> 32);  // listed counts, for the gather
-      nat += (u32)cv;
-    }
-    nat = block_sum(nat, L.s);
-    u64 ent[kFPer];
-    const u32 n = gather_lists(a, list_base(a, row), kLC, L.cties, ent, L);
+      nat = (u32)cv;
+      return (u32)(cv >> 32);  // listed tokens of the chunk
+    }, L, mx);
+    QS_TR(21);
     if (n == 0xffffffffu || n == 0u) {
       fine = false;
     } else {
-      // weights of the listed tokens and the exact boundary inside the bin
-      u32 wq[kFPer];  // packed weights
-      u32 bkmax = 0, bkmin = 0xffffffffu;
+      // the exact boundary among the listed tokens (in id order in L.u.fin.ent)
+      Held h;
+      hold_entries(L, n, h);
+      u32 wq[kFPer];
+      u32 bkmax = 0, bkmin = 0u;
 #pragma unroll
       for (int i = 0; i < kFPer; ++i) {
-        const u32 key = (u32)(ent[i] >> 32);
-        const bool in = threadIdx.x * kFPer + i < n;
-        u32 x = in ? wpack_of(f_of_key(key), key, qs, kstar, SH) : 0u;
-        x = wunpack(x) >= thr ? x : 0u;
-        wq[i] = x;
-        if (in) {
+        wq[i] = 0u;
+        if ((u32)i < h.per) {
+          const u32 key = (u32)(h.e[i] >> 32);
+          wq[i] = key ? wpk(key) : 0u;
           bkmax = max(bkmax, key);
-          bkmin = min(bkmin, key);
+          bkmin = key ? max(bkmin, ~key) : bkmin;
         }
       }
-      bkmax = block_max(bkmax, L.s);
-      bkmin = ~block_max(~bkmin, L.s);
-      Sel q;
-      sel_init(q, bkmin, bkmax, true, Tp - Ahi);
-      for (;;) {
-        sel_clear(L);
-        lds_sync();
-#pragma unroll
-        for (int i = 0; i < kFPer; ++i)
-          if (wq[i]) sel_add(q, L, (u32)(ent[i] >> 32), wunpack(wq[i]));
-        lds_sync();
-        if (sel_step(q, L)) break;
-      }
-      if (q.found != 1) {
+      block_max2(bkmax, bkmin, L.s);
+      nat = block_sum(nat, L.s);
+      bkmin = ~bkmin;
+      const SelRes q = held_select<true>(a, L, h, wq, max(bkmin, 1u), bkmax, Tp - Ahi);
+      if (!q.ok) {
         fine = false;
       } else {
         klo = q.kappa;
-        wt = q.kmass / q.kcount;
-        A = Ahi + q.above_m;
-        const u64 jj = (Tp - A) / wt + 1ull;
-        jties = (u32)(jj < (u64)q.kcount ? jj : (u64)q.kcount);
+        wt = wf(klo);  // every token at kappa_p has this weight
+        A = Ahi + q.mass_above;
+        const u64 jj = div_small(Tp - A, wt) + 1ull;
+        jties = (u32)(jj < (u64)q.cnt_at ? jj : (u64)q.cnt_at);
         W = A + (u64)jties * wt;
-        kept = nat + q.above_c + jties;
+        kept = nat + q.cnt_above + jties;
         // per chunk: listed mass above kappa_p and ties at it; the jties-th tie's id
         for (int cc = threadIdx.x; cc < a.G; cc += kThreads) L.cties[cc] = 0u;
         lds_sync();
         u32 tcount = 0;
 #pragma unroll
         for (int i = 0; i < kFPer; ++i) {
-          const u32 key = (u32)(ent[i] >> 32);
-          const int cc = (int)((u32)ent[i] / (u32)kCH);
-          if (wq[i] && key > klo) atomicAdd(&L.cmass[cc], wunpack(wq[i]));
-          if (wq[i] && key == klo) {
-            atomicAdd(&L.cties[cc], 1u);
-            ++tcount;
+          if ((u32)i < h.per) {
+            const u32 key = (u32)(h.e[i] >> 32);
+            const int cc = (int)((u32)h.e[i] / (u32)kCH);
+            if (wq[i] && key > klo) atomicAdd(&L.cmass[cc], wunpack(wq[i]));
+            if (wq[i] && key == klo) {
+              atomicAdd(&L.cties[cc], 1u);
+              ++tcount;
+            }
           }
         }
-        // id of the jties-th tie in id order (the list is in id order, thread-contiguous)
-        u32 tex, ttot;
-        tex = block_excl(tcount, L.s, &ttot);
+        // id of the jties-th tie in id order
+        u32 ttot;
+        u32 tex = block_excl(tcount, L.s, &ttot);
         if (threadIdx.x == 0) L.s.r[14] = (u32)a.V;
         lds_sync();
 #pragma unroll
         for (int i = 0; i < kFPer; ++i) {
-          const u32 key = (u32)(ent[i] >> 32);
-          if (wq[i] && key == klo) {
-            ++tex;
-            if (tex == jties) L.s.r[14] = (u32)ent[i];
+          if ((u32)i < h.per) {
+            const u32 key = (u32)(h.e[i] >> 32);
+            if (wq[i] && key == klo) {
+              ++tex;
+              if (tex == jties) L.s.r[14] = (u32)h.e[i];
+            }
           }
         }
         lds_sync();
@@ -1451,47 +1773,63 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       }
     }
   }
-  QS_TR(10);
+  QS_TR(22);
   if (!fine) return kStList;
-  if (!p.topp) {
-    u64 tot = 0;
-    for (int cc = 0; cc < a.G; ++cc) tot += L.cmass[cc];
-    W = tot;
-  }
-  // the chunk holding the draw: kept(c) = cmass[c] + min(ties(c), jties left) * wt
-  const u64 t = mul_frac(W, p.u);
-  if (threadIdx.x == 0) {
-    u64 acc = 0;
-    u32 tb = 0;
-    int owner = -1;
-    u64 tin = 0;
-    u32 jl_owner = 0;
-    for (int cc = 0; cc < a.G; ++cc) {
-      const u32 tcn = L.cties[cc];
-      const u32 jl = jties == 0xffffffffu ? 0u : (jties > tb ? jties - tb : 0u);
-      const u64 kc = L.cmass[cc] + (u64)min(tcn, jl) * wt;
-      if (owner < 0 && t < acc + kc) {
-        owner = cc;
-        tin = t - acc;
-        jl_owner = jl;
-      }
-      acc += kc;
-      tb += tcn;
+  // the chunk holding the draw: kept(c) = cmass[c] + min(ties(c), jties left) * wt;
+  // one wave scans the chunks, four per lane
+  if (threadIdx.x < 64) {
+    const int l = (int)lane_id();
+    u64 km[4];
+    u32 tn[4], ts = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cc = 4 * l + i;
+      km[i] = cc < a.G ? L.cmass[cc] : 0ull;
+      tn[i] = cc < a.G ? L.cties[cc] : 0u;
+      ts += tn[i];
     }
-    L.s.r[15] = (u32)owner;
-    L.s.r64[13] = tin;
-    L.s.r[7] = jl_owner;
+    u32 tb = wave_incl_scan(ts) - ts;
+    u64 ks = 0;
+    u64 kc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32 jl = jties == 0xffffffffu ? 0u : (jties > tb ? jties - tb : 0u);
+      kc[i] = km[i] + (u64)min(tn[i], jl) * wt;
+      ks += kc[i];
+      tb += tn[i];
+    }
+    const u64 ki = wave_incl_scan64(ks);
+    const u64 Wt = readlane64(ki, 63);
+    if (!p.topp) W = Wt;
+    const u64 t = mul_frac(W, p.u);
+    u64 acc = ki - ks;
+    tb = wave_incl_scan(ts) - ts;
+    if (l == 0) L.s.r[15] = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32 jl = jties == 0xffffffffu ? 0u : (jties > tb ? jties - tb : 0u);
+      if (acc <= t && t < acc + kc[i]) {
+        L.s.r[15] = (u32)(4 * l + i);
+        L.s.r64[13] = t - acc;
+        L.s.r[7] = jl;
+      }
+      acc += kc[i];
+      tb += tn[i];
+    }
+    if (l == 0) L.s.r64[14] = W;
   }
   lds_sync();
   const int owner = (int)L.s.r[15];
   const u64 tin = L.s.r64[13];
   const u32 jl = L.s.r[7];
+  W = L.s.r64[14];
   lds_sync();
   if (owner < 0) return kStIncomplete;
-  QS_TR(11);
+  QS_TR(23);
   // re-read the owner chunk and locate the token
   load_chunk<DT>(a, row, owner, ch);
   if (p.pen) pen_build(p, owner, L);
+  u32 kq[E];
   chunk_qkeys<DT>(ch, p, L, owner, kq);
   if (p.pen) lds_sync();
   const bool ties_on = jties != 0xffffffffu;
@@ -1501,11 +1839,12 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     const bool above = ties_on ? kq[i] > klo : true;
     return KW{above ? w : 0ull, ties_on && w && kq[i] == klo};
   };
+  QS_TR(24);
   const int pick = chunk_locate<DT>(ch, kw, wt, jl, tin, L);
   if (pick < 0) return kStIncomplete;
   write_result(a, row, p, pick, W, thr, p.topp ? kPathMassTopP : kPathMassAll, 0u, kstar, p.topp ? klo : 1u,
                p.topp ? idlo : (u32)a.V, kept);
-  QS_TR(12);
+  QS_TR(25);
   return 0u;
 }
 

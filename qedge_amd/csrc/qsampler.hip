@@ -50,7 +50,7 @@ bool layout_for(int B, int V, Layout* L) {
   if (L->R > kStageCap) L->R = kStageCap;
   L->SH = shift_of(V);
   const long long cand = (long long)L->G * L->R;
-  const long long mass = (long long)L->G * (kNB + kNB / 2 + kLC);
+  const long long mass = (long long)L->G * (kNB + kLC);
   L->dpr = cand > mass ? cand : mass;
   // one row's block: counters, result, slots, data
   L->off_sync = 0;
