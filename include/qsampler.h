@@ -109,6 +109,42 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
 int qs_argmax(const void* logits, int64_t row_stride, int logits_dtype, int B, int V,
               int64_t* out_ids, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Decode-step bookkeeping after qs_sample, on the device (no host round trip),
+ * one thread per row.  Replaces the GPU staging of ModelRunner._publish_sample_ids
+ * (src/compute/model_runner.py:95-115), the copy of _read_sample_ids
+ * (src/compute/model_runner.py:122-135) and the stop check of
+ * Scheduler.postprocess (src/control/scheduler.py:304-322):
+ *
+ *  ids            i64[B] sampled ids (qs_sample's out_ids)
+ *  slots          i32[B] or NULL: row r's id goes to pending[slots[r]] (NULL: slot r;
+ *                 slots outside [0, n_pending) are skipped)
+ *  pending        i64[n_pending] or NULL: the fixed next-token slots (model_runner.py:35-37)
+ *  num_generated  i32[B]: completion tokens so far, incremented for rows with max_tokens > 0
+ *  min_tokens     i32[B] or NULL (0);  max_tokens  i32[B];  ignore_eos  u8[B] or NULL (0)
+ *  eos_id         end-of-sequence id (< 0: none)
+ *  finished       u8[B] or NULL, out: max_tokens <= 0, or after the increment
+ *                 n >= max_tokens, or (!ignore_eos && n >= min_tokens && id == eos_id)
+ *  host_ids       i64[B] or NULL: the device address of a host-mapped pinned
+ *                 buffer that receives the ids (the CPU mirror)
+ */
+int qs_step_finish(const int64_t* ids, int B, const int32_t* slots, int64_t* pending, int n_pending,
+                   int32_t* num_generated, const int32_t* min_tokens, const int32_t* max_tokens,
+                   const uint8_t* ignore_eos, int64_t eos_id, uint8_t* finished, int64_t* host_ids,
+                   hipStream_t stream);
+
+/*
+ * Appends the sampled ids to the device-resident token history that qs_sample
+ * reads (hist_ids [B, H], hist_len [B]): hist_ids[r, hist_len[r] % H] = ids[r],
+ * hist_len[r] += 1, for rows with active[r] != 0 (active may be NULL: every
+ * row).  The history is a ring of the last H ids; qs_sample uses the last
+ * min(hist_len, H) of them.  Replaces Sequence.append_token's history
+ * (src/data/sequence.py:177-179) for the penalties, so the ids are not
+ * re-staged from the host each step.
+ */
+int qs_history_append(int32_t* hist_ids, int B, int H, int32_t* hist_len, const int64_t* ids,
+                      const uint8_t* active, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,12 +56,12 @@ def load():
                               P, SZ, P]                 # workspace, bytes, stream
     lib.qs_argmax.restype = I
     lib.qs_argmax.argtypes = [P, I64, I, I, I, P, P, SZ, P]
-    if hasattr(lib, "qs_history_append"):
-        lib.qs_history_append.restype = I
-        lib.qs_history_append.argtypes = [P, I, I, P, P, P, P]
-    if hasattr(lib, "qs_step_finish"):
-        lib.qs_step_finish.restype = I
-        lib.qs_step_finish.argtypes = [P, I, P, P, I, P, P, P, P, P, I, P, P]
+    lib.qs_step_finish.restype = I
+    lib.qs_step_finish.argtypes = [P, I, P, P, I,            # ids, B, slots, pending, n_pending
+                                   P, P, P, P, I64,          # num_generated, min, max, ignore_eos, eos_id
+                                   P, P, P]                  # finished, host_ids, stream
+    lib.qs_history_append.restype = I
+    lib.qs_history_append.argtypes = [P, I, I, P, P, P, P]   # hist, B, H, hist_len, ids, active, stream
     _lib = lib
     return lib
 

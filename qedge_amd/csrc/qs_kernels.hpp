@@ -35,7 +35,7 @@ constexpr int kFPer = kFCap / kThreads;    // of them per finishing thread
 constexpr int kDirect = kThreads / 8;      // a selection bin this small is resolved by direct ranking
 constexpr int kNB = 256;                   // mass histogram bins (one per thread)
 constexpr int kRounds = 3;                 // bracket rounds before the exact path
-constexpr int kLC = 128;                   // bracket entries per chunk
+constexpr int kLC = 256;                   // bracket entries per chunk
 constexpr int kNBS = 1024;                 // select histogram bins
 constexpr int kStageCap = 1024;            // entries staged in LDS by one workgroup
 
@@ -1176,6 +1176,7 @@ struct MassBins {
   float x0, x1, s1, s2;
   int n1;
 };
+static_assert(kNB <= 256, "a bin index fits a byte");
 constexpr float kXMax = 44.5f;  // y = -x * log2(e) < -64 past it: weight 0
 constexpr float kXFine = 12.0f; // first round: the finer segment, [0, kXFine)
 __device__ __forceinline__ MassBins mass_bins_first(float D) {
@@ -1228,11 +1229,10 @@ __device__ __forceinline__ MassBins mass_bins_split(const MassBins& m, u32 b) {
   n.s2 = 0.0f;
   return n;
 }
-// Per-row data of top-k-off rows: bin masses [G][kNB] u64, then the listed
-// tokens [G][kLC].
-__device__ __forceinline__ u64* list_base(const Args& a, int row) {
-  return row_data(a, row) + (size_t)a.G * kNB;
-}
+// Per-row data of top-k-off rows: the row's bin masses [kRounds][kNB] u64
+// (summed by atomics), then the listed tokens [G][kLC].
+__device__ __forceinline__ u64* row_hist(const Args& a, int row) { return row_data(a, row); }
+__device__ __forceinline__ u64* list_base(const Args& a, int row) { return row_data(a, row) + (size_t)kRounds * kNB; }
 
 // ---------------------------------------------------------------- the streaming kernel
 
@@ -1457,6 +1457,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   const float qs = f_of_key(kstar);
   // first-round bins over x = q* - q in [0, D], D = min(q* - q_min, kXMax)
   MassBins mb = mass_bins_first(qs - f_of_key(kmin));
+  u64 Tp = 0, A = 0;  // floor(top_p * S), the mass above the bracket
   if (ok) {
     // weights (packed, kept in registers), the chunk's mass and (top-p) the
     // first-round mass histogram, in one pass
@@ -1465,8 +1466,11 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       lds_sync();
     }
     u32 wp[E];
+    u32 bq[E / 4];  // each token's bin of the current round, four per word
     u64 Sc = 0;
     u32 nz = 0, inb = 0;
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i) bq[i] = 0u;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const u32 k = L.u.kq[i * kThreads + threadIdx.x];
@@ -1478,7 +1482,11 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       Sc += x ? w : 0ull;
       nz += x ? 1u : 0u;
       inb |= (x ? 1u : 0u) << i;
-      if (p.topp && x) atomicAdd(&L.mh[mass_bin(q, k, qs, kstar, mb)], w);
+      if (p.topp && x) {
+        const u32 bi = mass_bin(q, k, qs, kstar, mb);
+        bq[i / 4] |= bi << (8 * (i % 4));
+        atomicAdd(&L.mh[bi], w);
+      }
     }
     QS_TR(5);
     block_sum2(Sc, nz, L.s);  // its barriers also complete the histogram
@@ -1488,125 +1496,76 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     }
     QS_TR(6);
     if (p.topp) {
-      // Bracket the top-p boundary: each round's mass histogram of the tokens
-      // still in the bracket is published; the last workgroup to arrive (the
-      // reducer) picks the bin holding the boundary and either has it listed
-      // (few enough tokens, bounded by the bin's mass over its least weight)
-      // or has every workgroup split it again.
+      // Bracket the top-p boundary: each round, every workgroup adds its mass
+      // histogram of the tokens still in the bracket to the row's (atomics),
+      // waits for the row, and reads it; the bin holding the boundary is either
+      // listed (few enough tokens, bounded by the bin's mass over its least
+      // weight) or split again.  Every workgroup decides alike.
       u32 abv = 0;  // tokens above the bracket
-      u64* hm_g = row_data(a, row);
+      u64* hr = row_hist(a, row);
       bool listed = false;
       for (int r = 0; r < kRounds && ok && !listed; ++r) {
         if (r > 0) {
           for (int b = threadIdx.x; b < kNB; b += kThreads) L.mh[b] = 0ull;
           lds_sync();
 #pragma unroll
+          for (int i = 0; i < E / 4; ++i) bq[i] = 0u;
+#pragma unroll
           for (int i = 0; i < E; ++i) {
-            if ((inb >> i) & 1u)
-              atomicAdd(&L.mh[mass_bin(f_of_key(L.u.kq[i * kThreads + threadIdx.x]), L.u.kq[i * kThreads + threadIdx.x], qs, kstar, mb)], wunpack(wp[i]));
+            if ((inb >> i) & 1u) {
+              const u32 k = L.u.kq[i * kThreads + threadIdx.x];
+              const u32 bi = mass_bin(f_of_key(k), k, qs, kstar, mb);
+              bq[i / 4] |= bi << (8 * (i % 4));
+              atomicAdd(&L.mh[bi], wunpack(wp[i]));
+            }
           }
           lds_sync();
         }
         QS_TR(7 + 4 * r);
-        for (int b = threadIdx.x; b < kNB; b += kThreads) stc(&hm_g[(size_t)c * kNB + b], L.mh[b]);
-        const u32 before = arrive(&sy->barB, L.s);
+        for (int b = threadIdx.x; b < kNB; b += kThreads) {
+          const u64 v = L.mh[b];
+          if (v) addc(&hr[(size_t)r * kNB + b], v);
+        }
+        (void)arrive(&sy->barB, L.s);
         QS_TR(8 + 4 * r);
-        if (before == (u32)a.G * (u32)(r + 1) - 1u) {
-          // the reducer: per bin the total over the chunks and the largest
-          // chunk share (thread t: bin t % kNB, every second chunk from t / kNB)
-          static_assert(kThreads == 2 * kNB, "two threads per bin");
-          const int b = threadIdx.x & (kNB - 1), h = threadIdx.x / kNB;
-          u64 bm = 0, bx = 0;
-          for (int c0 = h; c0 < a.G; c0 += 16) {
-            u64 v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int cc = c0 + 2 * j;
-              v[j] = cc < a.G ? ldc(&hm_g[(size_t)cc * kNB + b]) : 0ull;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              bm += v[j];
-              bx = v[j] > bx ? v[j] : bx;
-            }
-          }
-          if (h == 1) {
-            L.sel.hm[b] = bm;
-            L.sel.hm[kNB + b] = bx;
-          }
-          lds_sync();
-          if (h == 0) {
-            bm += L.sel.hm[b];
-            bx = L.sel.hm[kNB + b] > bx ? L.sel.hm[kNB + b] : bx;
-          } else {
-            bm = bx = 0ull;
-          }
-          u64 tot;
-          const u64 ex = block_excl64(bm, L.s, &tot);
-          u64 Tp, A;
-          if (r == 0) {
-            Tp = mul_frac(tot, p.tp);
-            A = 0;
-          } else {
-            Tp = ldc(&a.res[row].Tp);
-            A = ldc(&a.res[row].Ahi);
-          }
-          const u64 target = Tp - A;
-          if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
-          lds_sync();
-          if (h == 0 && ex <= target && target < ex + bm) {
-            L.s.r[12] = (u32)b;
-            L.s.r64[12] = ex;
-            // tokens of the bin: at most its mass over its least weight
-            const float wl = bin_least_weight(mb, b, SH);
-            const float nb = wl > 0.0f ? (float)bm / wl : 3.0e38f, nx = wl > 0.0f ? (float)bx / wl : 3.0e38f;
-            L.s.r[13] = (nb <= (float)kFCap && nx <= (float)kLC) ? 1u : 0u;
-          }
-          lds_sync();
-          const u32 bsel = L.s.r[12];
-          if (threadIdx.x == 0) {
-            RowRes* rr = &a.res[row];
-            u32 act;  // 1: list the bin, 0: split it again, 2: give up (the exact path resolves the row)
-            if (bsel == 0xffffffffu) {
-              act = 2;
-            } else {
-              act = L.s.r[13] ? 1u : (r + 1 < kRounds ? 0u : 2u);
-              if (r == 0) {
-                stc(&rr->Tp, Tp);
-                stc(&rr->S, tot);
-              }
-              stc(&rr->Ahi, A + L.s.r64[12]);
-            }
-            if (act == 2) orc(&sy->status, kStList);
-            wait_mem();
-            stc(&sy->dec, ((u32)(r + 1) << 16) | (act << 14) | (bsel & 0x3fffu));
-          }
-          lds_sync();
-        } else {
-          ok = wait_count(a, row, &sy->dec, (u32)(r + 1) << 16, L.s);
-        }
+        ok = wait_count(a, row, &sy->barB, (u32)a.G * (u32)(r + 1), L.s);
         QS_TR(9 + 4 * r);
-        if (ok) {
-          if (threadIdx.x == 0) L.s.r[15] = ldc(&sy->dec);
-          lds_sync();
-          const u32 dv = L.s.r[15];
-          lds_sync();
-          const u32 act = (dv >> 14) & 3u, bsel = dv & 0x3fffu;
-          if (act == 2u) {
-            ok = false;
-          } else {
-#pragma unroll
-            for (int i = 0; i < E; ++i) {
-              if ((inb >> i) & 1u) {
-                const u32 b = mass_bin(f_of_key(L.u.kq[i * kThreads + threadIdx.x]), L.u.kq[i * kThreads + threadIdx.x], qs, kstar, mb);
-                if (b < bsel) abv |= 1u << i;
-                if (b != bsel) inb &= ~(1u << i);
-              }
-            }
-            listed = act == 1u;
-            mb = mass_bins_split(mb, bsel);
-          }
+        if (!ok) break;
+        // the row's bins: the crossing bin and the mass above it
+        const int b = threadIdx.x;
+        const u64 bm = b < kNB ? ldc(&hr[(size_t)r * kNB + b]) : 0ull;
+        u64 tot;
+        const u64 ex = block_excl64(bm, L.s, &tot);
+        if (r == 0) Tp = mul_frac(tot, p.tp);
+        const u64 target = Tp - A;
+        if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
+        lds_sync();
+        if (b < kNB && ex <= target && target < ex + bm) {
+          L.s.r[12] = (u32)b;
+          L.s.r64[12] = ex;
+          // tokens of the bin: at most its mass over its least weight
+          const float wl = bin_least_weight(mb, b, SH);
+          L.s.r[13] = (float)bm <= wl * (float)kFCap ? 1u : 0u;
         }
+        lds_sync();
+        const u32 bsel = uni(L.s.r[12]);
+        const u32 small = uni(L.s.r[13]);
+        const u64 exs = uni64(L.s.r64[12]);
+        lds_sync();
+        if (bsel == 0xffffffffu || (!small && r + 1 == kRounds)) {
+          fail_row(a, row, kStList);
+          ok = false;
+          break;
+        }
+        A += exs;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const u32 bi = (bq[i / 4] >> (8 * (i % 4))) & 0xffu;
+          if (((inb >> i) & 1u) && bi < bsel) abv |= 1u << i;
+          if (bi != bsel) inb &= ~(1u << i);
+        }
+        listed = small != 0u;
+        mb = mass_bins_split(mb, bsel);
         QS_TR(10 + 4 * r);
       }
       if (ok) {
@@ -1674,10 +1633,14 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return kNotLast;
   QS_TR(20);
   // ---- the row's last workgroup: the selector
+  if (p.topp) {  // every workgroup is past the row histograms: back to zero
+    u64* hr = row_hist(a, row);
+    for (int i = threadIdx.x; i < kRounds * kNB; i += kThreads) stc(&hr[i], 0ull);
+  }
   const u32 st = ldc(&sy->status);
   if (st != 0u || kstar == 0u) return st ? st : kStIncomplete;
   // per-chunk kept masses and tie counts in L.cmass / L.cties
-  u64 W = 0, Tp = 0, A = 0, wt = 0;
+  u64 W = 0, wt = 0;
   u32 klo = 1u, jties = 0xffffffffu, kept = 0, idlo = (u32)a.V;
   bool fine = true;
   auto wpk = [&](u32 key) -> u32 {
@@ -1694,8 +1657,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     }
     kept = block_sum(nzt, L.s);
   } else {
-    Tp = ldc(&a.res[row].Tp);
-    const u64 Ahi = ldc(&a.res[row].Ahi);
+    const u64 Ahi = A;
     u32 nat = 0;
     u32 mx[3];
     const u32 n = gather_lds(a, list_base(a, row), kLC, [&](int cc, u32(&)[3]) -> u32 {

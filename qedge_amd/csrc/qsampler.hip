@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include "qs_kernels.hpp"
+#include "qs_step.hpp"
 #include "qsampler.h"
 
 namespace {
@@ -50,7 +51,7 @@ bool layout_for(int B, int V, Layout* L) {
   if (L->R > kStageCap) L->R = kStageCap;
   L->SH = shift_of(V);
   const long long cand = (long long)L->G * L->R;
-  const long long mass = (long long)L->G * (kNB + kLC);
+  const long long mass = (long long)kRounds * kNB + (long long)L->G * kLC;
   L->dpr = cand > mass ? cand : mass;
   // one row's block: counters, result, slots, data
   L->off_sync = 0;
@@ -200,6 +201,48 @@ int qs_argmax(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   return qs_sample(logits, row_stride, logits_dtype, B, V, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                    nullptr, nullptr, 0, nullptr, nullptr, nullptr, QS_FLAG_ALL_GREEDY, out_ids, nullptr, nullptr,
                    workspace, workspace_bytes, stream);
+}
+
+int qs_step_finish(const int64_t* ids, int B, const int32_t* slots, int64_t* pending, int n_pending,
+                   int32_t* num_generated, const int32_t* min_tokens, const int32_t* max_tokens,
+                   const uint8_t* ignore_eos, int64_t eos_id, uint8_t* finished, int64_t* host_ids,
+                   hipStream_t stream) {
+  g_err[0] = 0;
+  if (B < 0) return fail("qs_step_finish: B < 0 (%lld)", B);
+  if (B == 0) return 0;
+  if (!ids || !num_generated || !max_tokens) return fail("qs_step_finish: ids, num_generated and max_tokens are required");
+  if (pending && n_pending <= 0) return fail("qs_step_finish: pending needs n_pending > 0 (%lld)", n_pending);
+  StepArgs a;
+  a.ids = (const long long*)ids;
+  a.B = B;
+  a.slots = slots;
+  a.pending = (long long*)pending;
+  a.n_pending = pending ? n_pending : 0;
+  a.num_generated = num_generated;
+  a.min_tokens = min_tokens;
+  a.max_tokens = max_tokens;
+  a.ignore_eos = ignore_eos;
+  a.eos_id = eos_id;
+  a.finished = finished;
+  a.host_ids = (long long*)host_ids;
+  hipLaunchKernelGGL(k_step_finish, dim3((B + 255) / 256), dim3(256), 0, stream, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("qs_step_finish: launch failed (%lld)", (long long)e);
+  return 0;
+}
+
+int qs_history_append(int32_t* hist_ids, int B, int H, int32_t* hist_len, const int64_t* ids,
+                      const uint8_t* active, hipStream_t stream) {
+  g_err[0] = 0;
+  if (B < 0) return fail("qs_history_append: B < 0 (%lld)", B);
+  if (B == 0) return 0;
+  if (H <= 0 || H > QS_MAX_HISTORY) return fail("qs_history_append: H out of range (%lld)", H);
+  if (!hist_ids || !hist_len || !ids) return fail("qs_history_append: hist_ids, hist_len and ids are required");
+  hipLaunchKernelGGL(k_history_append, dim3((B + 255) / 256), dim3(256), 0, stream, hist_ids, B, H, hist_len,
+                     (const long long*)ids, active);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("qs_history_append: launch failed (%lld)", (long long)e);
+  return 0;
 }
 
 }  // extern "C"
