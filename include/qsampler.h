@@ -102,6 +102,25 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
               int32_t* out_kept, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * qs_sample without a workspace argument, for callers that cannot allocate
+ * device memory (code under graph capture, fixed serving loops, harnesses that
+ * forbid allocation).  It has no counterpart in the reference.  The scratch is
+ * the library's own device array of qs_static_scratch_bytes() bytes (32 MiB)
+ * on each GPU, held until the process ends; a batch whose workspace would not
+ * fit in it is rejected with an error.  The first call on a device clears the
+ * array with a fill kernel on `stream`; every call leaves it cleared.  Calls
+ * that overlap on one GPU share the array and race: serialise them.
+ * Allocates nothing (no hipMalloc, no library allocation).
+ */
+int qs_sample_static(const void* logits, int64_t row_stride, int logits_dtype, int B, int V,
+                     const float* temperature, const float* top_p, const int32_t* top_k, const float* min_p,
+                     const float* rep_pen, const float* pres_pen, const float* freq_pen,
+                     const int32_t* hist_ids, int H, const int32_t* hist_len, const float* uniforms,
+                     const int32_t* row_order, uint32_t flags, int64_t* out_ids, float* out_probs,
+                     int32_t* out_kept, hipStream_t stream);
+size_t qs_static_scratch_bytes(void);
+
+/*
  * Greedy ids only: first index of the maximum logit per row, NaN is maximum.
  * Replaces logits.argmax(-1) on the all-greedy path and inside the captured
  * decode graph (src/compute/model_runner.py:85,353).

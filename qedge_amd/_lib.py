@@ -21,7 +21,7 @@ QS_TOPK_FAST_MAX = 1024
 QS_MAX_HISTORY = 65535
 
 EXPORTS = ("qs_version", "qs_last_error", "qs_workspace_bytes", "qs_workspace_init", "qs_sample", "qs_argmax",
-           "qs_history_append", "qs_step_finish")
+           "qs_history_append", "qs_step_finish", "qs_sample_static", "qs_static_scratch_bytes")
 
 _lib = None
 
@@ -56,6 +56,10 @@ def load():
                               P, SZ, P]                 # workspace, bytes, stream
     lib.qs_argmax.restype = I
     lib.qs_argmax.argtypes = [P, I64, I, I, I, P, P, SZ, P]
+    lib.qs_sample_static.restype = I
+    lib.qs_sample_static.argtypes = lib.qs_sample.argtypes[:-3] + [P]  # no workspace: the library's scratch
+    lib.qs_static_scratch_bytes.restype = SZ
+    lib.qs_static_scratch_bytes.argtypes = []
     lib.qs_step_finish.restype = I
     lib.qs_step_finish.argtypes = [P, I, P, P, I,            # ids, B, slots, pending, n_pending
                                    P, P, P, P, I64,          # num_generated, min, max, ignore_eos, eos_id

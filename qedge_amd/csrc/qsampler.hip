@@ -85,6 +85,14 @@ int max_rows_of(size_t bytes, int V) {
   return b;
 }
 
+// Library-owned scratch for qs_sample_static (callers that cannot allocate).
+// In host code `scratch` names a host-side stand-in: the device address of each
+// GPU's copy comes from hipGetSymbolAddress, once per device.
+constexpr size_t kStaticScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
 
 extern "C" {
@@ -195,6 +203,38 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   }
   return 0;
 }
+
+int qs_sample_static(const void* logits, int64_t row_stride, int logits_dtype, int B, int V,
+                     const float* temperature, const float* top_p, const int32_t* top_k, const float* min_p,
+                     const float* rep_pen, const float* pres_pen, const float* freq_pen,
+                     const int32_t* hist_ids, int H, const int32_t* hist_len, const float* uniforms,
+                     const int32_t* row_order, uint32_t flags, int64_t* out_ids, float* out_probs,
+                     int32_t* out_kept, hipStream_t stream) {
+  g_err[0] = 0;
+  if (B < 0) return fail("qs_sample_static: B < 0 (%lld)", B);
+  if (B == 0) return 0;
+  Layout L;
+  if (V <= 0 || !layout_for(B, V, &L)) return fail("qs_sample_static: no layout for V = %lld", V);
+  if (max_rows_of(kStaticScratchBytes, V) < B)
+    return fail("qs_sample_static: the batch needs more than the static scratch (%lld bytes)",
+                (long long)kStaticScratchBytes);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail("qs_sample_static: no current device (%lld)", dev);
+  if (!g_scratch_ptr[dev]) {
+    // first call on this device: the address of its copy, cleared once by a fill kernel
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return fail("qs_sample_static: hipGetSymbolAddress failed (%lld)", (long long)e);
+    if (qs_workspace_init(ptr, kStaticScratchBytes, stream) != 0) return -1;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return qs_sample(logits, row_stride, logits_dtype, B, V, temperature, top_p, top_k, min_p, rep_pen, pres_pen,
+                   freq_pen, hist_ids, H, hist_len, uniforms, row_order, flags, out_ids, out_probs, out_kept,
+                   g_scratch_ptr[dev], kStaticScratchBytes, stream);
+}
+
+size_t qs_static_scratch_bytes(void) { return kStaticScratchBytes; }
 
 int qs_argmax(const void* logits, int64_t row_stride, int logits_dtype, int B, int V, int64_t* out_ids,
               void* workspace, size_t workspace_bytes, hipStream_t stream) {
