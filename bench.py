@@ -65,8 +65,10 @@ class Case:
         self.R = R = max(1, min(max_copies, math.ceil(rotate_bytes / nbytes)))
         self.logits = [base] + [base.clone() for _ in range(R - 1)]
         t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)
+        topk_on = bool(np.any((w.top_k > 0) & (w.top_k < V)))  # as SamplingBatch.use_top_k
         self.params = dict(temperatures=t(w.temperature, torch.float32), top_ps=t(w.top_p, torch.float32),
-                           top_ks=t(w.top_k, torch.int32), repetition_penalties=t(w.rep, torch.float32),
+                           top_ks=t(w.top_k, torch.int32) if topk_on else None,
+                           repetition_penalties=t(w.rep, torch.float32),
                            presence_penalties=t(w.pres, torch.float32),
                            frequency_penalties=t(w.freq, torch.float32), history=t(w.history, torch.int32))
         self.uniforms = [t(w.uniforms(s), torch.float32) for s in range(R)]

@@ -17,6 +17,7 @@ QS_DTYPE_BF16 = 1
 QS_FLAG_ALL_GREEDY = 1
 QS_FLAG_USE_TOP_P = 2
 QS_FLAG_NO_WAIT = 4
+QS_FLAG_SOLO = 8
 QS_TOPK_FAST_MAX = 1024
 QS_MAX_HISTORY = 65535
 

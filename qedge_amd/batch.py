@@ -169,9 +169,10 @@ class SamplingBatch:
     def sampler_kwargs(self, with_history: bool = True) -> dict:
         """Keyword arguments for ``BatchSampler.forward`` / ``sample_into`` (rows [:bs])."""
         bs = self.bs
-        kw = dict(temperatures=self.temperatures[:bs], top_ps=self.top_ps[:bs], top_ks=self.top_ks[:bs],
-                  uniforms=self.uniforms[:bs], all_greedy=self.all_greedy, use_top_p=self.use_top_p,
-                  row_order=self.row_order[:bs])
+        kw = dict(temperatures=self.temperatures[:bs], top_ps=self.top_ps[:bs], uniforms=self.uniforms[:bs],
+                  all_greedy=self.all_greedy, use_top_p=self.use_top_p, row_order=self.row_order[:bs])
+        if self.use_top_k:
+            kw["top_ks"] = self.top_ks[:bs]
         if self.use_min_p:
             kw["min_ps"] = self.min_ps[:bs]
         if self.use_penalties:

@@ -44,7 +44,7 @@ constexpr u32 kWhyLargeK = 16u;          // top-k above kTopkMax
 constexpr u32 kNotLast = 0xffffffffu;    // not the row's last workgroup
 enum : u32 { kKindGreedy = 0, kKindTopK = 1, kKindMass = 2, kKindSingle = 3 };
 // How the last call resolved a row (RowRes::path).
-enum : u32 { kPathGreedy = 1, kPathTopK = 2, kPathMassTopP = 3, kPathMassAll = 4, kPathSingle = 5 };
+enum : u32 { kPathGreedy = 1, kPathTopK = 2, kPathMassTopP = 3, kPathMassAll = 4, kPathSingle = 5, kPathSolo = 6 };
 
 // Per-row counters, each on its own 128-byte line.  Zero between calls.
 struct __attribute__((aligned(128))) RowSync {
@@ -130,23 +130,27 @@ struct RowP {
   const int* hist;
 };
 
+// Row parameters, moved to scalar registers: every branch on them is uniform.
+__device__ __forceinline__ float unif(float v) { return __uint_as_float(uni(__float_as_uint(v))); }
 __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   RowP p;
-  p.T = a.temperature ? gld(a.temperature + row) : 0.0f;
+  row = (int)uni((u32)row);
+  p.T = a.temperature ? unif(gld(a.temperature + row)) : 0.0f;
   const bool greedy = (a.flags & QS_FLAG_ALL_GREEDY) || (p.T <= 1e-5f);
-  p.k = a.top_k ? gld(a.top_k + row) : 0;
+  p.k = a.top_k ? (int)uni((u32)gld(a.top_k + row)) : 0;
   const bool topk_on = p.k > 0 && p.k < a.V;
-  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? gld(a.top_p + row) : 1.0f;
+  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? unif(gld(a.top_p + row)) : 1.0f;
   p.topp = p.tp < 1.0f;
-  p.mp = a.min_p ? gld(a.min_p + row) : 0.0f;
-  p.rep = a.rep ? gld(a.rep + row) : 1.0f;
-  p.pres = a.pres ? gld(a.pres + row) : 0.0f;
-  p.freq = a.freq ? gld(a.freq + row) : 0.0f;
-  p.hlen = a.hist ? (a.hist_len ? gld(a.hist_len + row) : a.H) : 0;
+  p.mp = a.min_p ? unif(gld(a.min_p + row)) : 0.0f;
+  p.rep = a.rep ? unif(gld(a.rep + row)) : 1.0f;
+  p.pres = a.pres ? unif(gld(a.pres + row)) : 0.0f;
+  p.freq = a.freq ? unif(gld(a.freq + row)) : 0.0f;
+  p.hlen = a.hist ? (a.hist_len ? (int)uni((u32)gld(a.hist_len + row)) : a.H) : 0;
   if (p.hlen > a.H) p.hlen = a.H;
+  if (p.hlen < 0) p.hlen = 0;
   p.hist = a.hist ? a.hist + (size_t)row * a.H : nullptr;
   p.pen = p.hist != nullptr && p.hlen > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
-  p.u = a.uniforms ? gld(a.uniforms + row) : 0.0f;
+  p.u = a.uniforms ? unif(gld(a.uniforms + row)) : 0.0f;
   if (!(p.u >= 0.0f)) p.u = 0.0f;
   if (p.u >= 1.0f) p.u = __uint_as_float(0x3f7fffffu);
   p.kind = greedy ? kKindGreedy : (topk_on ? (p.k <= kTopkMax ? kKindTopK : kKindSingle) : kKindMass);
@@ -237,27 +241,35 @@ __device__ __forceinline__ void load_chunk(const Args& a, int row, int c, Chunk<
   }
 }
 
+// The chunk's history-count table (two 16-bit counts per word) of an LDS layout.
+__device__ __forceinline__ u32* pen_table(Lds& L) { return L.u.pen; }
+__device__ __forceinline__ const u32* pen_table(const Lds& L) { return L.u.pen; }
+// The i-th history id of the row (overloads may keep a copy in LDS).
+__device__ __forceinline__ int hist_id(const RowP& p, const Lds&, int i) { return gld(p.hist + i); }
+
 // History counts of the ids in [c*kCH, (c+1)*kCH) into the LDS table.
-__device__ __forceinline__ void pen_build(const RowP& p, int c, Lds& L) {
-  uint4* t4 = (uint4*)L.u.pen;
+template <typename LT>
+__device__ __forceinline__ void pen_build(const RowP& p, int c, LT& L) {
+  u32* t = pen_table(L);
+  uint4* t4 = (uint4*)t;
   for (int i = threadIdx.x; i < kCH / 8; i += kThreads) t4[i] = make_uint4(0u, 0u, 0u, 0u);
   lds_sync();
   const int lo = c * kCH;
   for (int i = threadIdx.x; i < p.hlen; i += kThreads) {
-    const int d = gld(p.hist + i) - lo;
-    if ((unsigned)d < (unsigned)kCH) atomicAdd(&L.u.pen[d >> 1], (d & 1) ? 0x10000u : 1u);
+    const int d = hist_id(p, L, i) - lo;
+    if ((unsigned)d < (unsigned)kCH) atomicAdd(&t[d >> 1], (d & 1) ? 0x10000u : 1u);
   }
   lds_sync();
 }
 // Count of element (j, e) of the thread from the table.
-template <int DT>
-__device__ __forceinline__ u32 pen_count(const Lds& L, const Chunk<DT>& ch, int c, int j, int e) {
+template <int DT, typename LT>
+__device__ __forceinline__ u32 pen_count(const LT& L, const Chunk<DT>& ch, int c, int j, int e) {
   const int li = ch.base - c * kCH + j * 64 * Chunk<DT>::VL + e;
-  return (L.u.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
+  return (pen_table(L)[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
 }
 // z of element (j, e): the logit with the penalties applied.
-template <int DT>
-__device__ __forceinline__ float elem_z(const Chunk<DT>& ch, const RowP& p, const Lds& L, int c, int j, int e) {
+template <int DT, typename LT>
+__device__ __forceinline__ float elem_z(const Chunk<DT>& ch, const RowP& p, const LT& L, int c, int j, int e) {
   float z = ch.raw(j, e);
   if (p.pen) {
     const u32 n = pen_count(L, ch, c, j, e);
@@ -266,8 +278,8 @@ __device__ __forceinline__ float elem_z(const Chunk<DT>& ch, const RowP& p, cons
   return z;
 }
 // Keys of q = z / T for every element (0 for NaN and invalid elements).
-template <int DT>
-__device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, const Lds& L, int c, u32 (&kq)[kEPT]) {
+template <int DT, typename LT>
+__device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, const LT& L, int c, u32 (&kq)[kEPT]) {
 #pragma unroll
   for (int j = 0; j < Chunk<DT>::J; ++j)
 #pragma unroll
@@ -848,7 +860,8 @@ struct Held {
   u64 e[kFPer];
   u32 per;  // uniform
 };
-__device__ __forceinline__ void hold_entries(const Lds& L, u32 n, Held& h) {
+template <typename LT>
+__device__ __forceinline__ void hold_entries(const LT& L, u32 n, Held& h) {
   h.per = uni((n + kThreads - 1) / kThreads);
   const u32 i0 = threadIdx.x * h.per;
 #pragma unroll
@@ -881,8 +894,8 @@ struct SelRes {
   u64 mass_above, mass_at;
   bool ok;
 };
-template <bool BY_MASS>
-__device__ __forceinline__ SelRes held_select(const Args& a, Lds& L, const Held& h, const u32 (&wq)[kFPer], u32 lo,
+template <bool BY_MASS, typename LT>
+__device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& h, const u32 (&wq)[kFPer], u32 lo,
                                               u32 hi, u64 target) {
   (void)a;
   SelRes r;
@@ -1816,7 +1829,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   __shared__ Lds L;
   constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
   const int c = blockIdx.x;
-  const int row = a.order ? gld(a.order + blockIdx.y) : (int)blockIdx.y;
+  const int row = (int)uni(a.order ? (u32)gld(a.order + blockIdx.y) : blockIdx.y);
   if ((unsigned)row >= (unsigned)a.B) return;  // row_order must be a permutation of [0, B)
   QS_TR(0);
   Chunk<DT> ch;

@@ -1,0 +1,597 @@
+// One workgroup per row, for large batches: the workgroup streams its row in
+// passes with the next chunk's loads in flight while it works on the current
+// one, and needs no other workgroup.  Same contract and results as k_sample.
+//
+//   pass 1  key range of q (and the greedy id)
+//   top-k   the k-th largest key: passes histogramming the keys (256 bins)
+//           until the bin holds one key
+//   pass 2  weights: S, the per-segment masses, the first mass histogram
+//   rounds  while the bin holding the top-p boundary is too large: one more
+//           pass histograms the bin's tokens by key (256 bins, counts and mass)
+//   pass 3  the bracket's tokens listed (key, id) in LDS, the mass above it per
+//           segment (a segment is one wave's vector span of one chunk: 64 * VL ids)
+//   final   the exact boundary among the listed tokens, the segment holding the
+//           draw, and the token inside it from one wave's re-read of the segment.
+#pragma once
+
+#include "qs_kernels.hpp"
+
+namespace qs {
+
+constexpr int kSoloList = 2048;   // bracket tokens listed in LDS
+constexpr int kSoloSegs = 1024;   // segments per row (G * kWaves * J)
+constexpr int kSoloRounds = 6;    // bracket rounds: the first in x = q* - q, then in key space
+constexpr int kSoloHist = 4096;   // history ids copied to LDS (the rest are read from memory)
+
+struct SoloFin {
+  u64 ent[kSoloList];  // listed tokens (key << 32 | id), in no particular order
+  u32 lk[kDirect];     // a select bin's keys for the direct resolution
+  u64 lw[kDirect];
+};
+struct SoloSel {
+  u32 hc[kNB];
+  u64 hm[kNB];
+};
+struct SoloLds {
+  union {
+    SoloFin fin;
+  } u;
+  u32 pen[kCH / 2];      // the chunk's history counts
+  int hist[kSoloHist];   // the row's history ids
+  SoloSel sel;           // select histogram of the final selection
+  u64 mh[kNB];           // bracket histogram: mass per bin
+  u32 hc[kNB];           // and tokens per bin (key-space rounds)
+  u64 seg[kSoloSegs];    // per segment: total mass, then the mass above the bracket, then kept mass
+  u32 segt[kSoloSegs];   // per segment: tokens at the boundary key (a bracket of one key)
+  u32 nlist;
+  Scratch s;
+};
+
+__device__ __forceinline__ u32* pen_table(SoloLds& L) { return L.pen; }
+__device__ __forceinline__ const u32* pen_table(const SoloLds& L) { return L.pen; }
+__device__ __forceinline__ int hist_id(const RowP& p, const SoloLds& L, int i) {
+  return i < kSoloHist ? L.hist[i] : gld(p.hist + i);
+}
+
+// Segment of a token id: one wave's vector span (64 * VL ids) of a chunk.
+template <int DT>
+__device__ __forceinline__ int seg_of(int id) {
+  return id / (64 * Chunk<DT>::VL);
+}
+
+// f(ch, c) over the row's chunks, with chunk c + 1's loads in flight during
+// chunk c and the history table built per chunk.
+template <int DT, typename F>
+__device__ __forceinline__ void solo_pass(const Args& a, const RowP& p, int row, SoloLds& L, F&& f) {
+  Chunk<DT> b0, b1;
+  load_chunk<DT>(a, row, 0, b0);
+  for (int c = 0; c < a.G; c += 2) {
+    if (c + 1 < a.G) load_chunk<DT>(a, row, c + 1, b1);
+    if (p.pen) pen_build(p, c, L);
+    f(b0, c);
+    if (p.pen) lds_sync();
+    if (c + 1 >= a.G) break;
+    if (c + 2 < a.G) load_chunk<DT>(a, row, c + 2, b0);
+    if (p.pen) pen_build(p, c + 1, L);
+    f(b1, c + 1);
+    if (p.pen) lds_sync();
+  }
+}
+
+// The bracket: tokens with mass_bin(q; mb0) == b0 and key in [lo, hi].  The
+// key bounds start as an estimate of bin b0's key range; the key-space rounds
+// put the tokens of bin b0 outside [lo, hi] in their first or last bin, so
+// every token of bin b0 is accounted for whatever the estimate.
+struct Bracket {
+  MassBins mb0;
+  u32 b0, lo, hi;
+};
+// Key-space bin of round r >= 1 for a key of bin b0 (range [lo, hi], width 2^sh per bin).
+__device__ __forceinline__ u32 key_bin(u32 k, u32 lo, u32 hi, int sh) {
+  return k > hi ? 0u : (k < lo ? (u32)kNB - 1u : (hi - k) >> sh);
+}
+// 0: above the bracket, 1: in it, 2: below it.
+__device__ __forceinline__ int bracket_side(const Bracket& br, float q, u32 k, float qs, u32 ks) {
+  const u32 b = mass_bin(q, k, qs, ks, br.mb0);
+  if (b != br.b0) return b < br.b0 ? 0 : 2;
+  return k > br.hi ? 0 : (k < br.lo ? 2 : 1);
+}
+
+// One wave re-reads segment s and returns, to every lane, the id of the token
+// at which the inclusive id-order total of val(z, key, id) passes t (or -1).
+// The chunk's history table must be built.
+template <int DT, typename VF>
+__device__ __forceinline__ long long seg_find(const Args& a, const RowP& p, int row, const SoloLds& L, int s, u64 t,
+                                              VF&& val) {
+  constexpr int VL = Chunk<DT>::VL, J = Chunk<DT>::J;
+  const int c = s / (kWaves * J), w = (s / J) % kWaves, j = s % J;
+  const int l = lane_id();
+  const int i0 = c * kCH + w * kWaveSpan + j * 64 * VL + l * VL;
+  const size_t rowoff = (size_t)row * (size_t)a.row_stride;
+  u32 x[4] = {0u, 0u, 0u, 0u};
+  if (a.vec_ok && i0 + VL <= a.V) {
+    const uint4 v = DT == QS_DTYPE_F32 ? gld((const uint4*)((const float*)a.logits + rowoff + i0))
+                                       : gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+  } else if (DT == QS_DTYPE_F32) {
+    const float* q = (const float*)a.logits + rowoff;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (i0 + e < a.V) x[e] = __float_as_uint(gld(q + i0 + e));
+  } else {
+    const uint16_t* q = (const uint16_t*)a.logits + rowoff;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < a.V) x[e >> 1] |= (u32)gld(q + i0 + e) << ((e & 1) * 16);
+  }
+  u64 v[VL];
+  u64 tot = 0;
+#pragma unroll
+  for (int e = 0; e < VL; ++e) {
+    const int id = i0 + e;
+    float z = DT == QS_DTYPE_F32 ? __uint_as_float(x[e]) : bf16_to_f32((x[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+    if (p.pen) {
+      const int li = id - c * kCH;
+      const u32 n = (L.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
+      if (n) z = apply_penalty(z, n, p.rep, p.pres, p.freq);
+    }
+    v[e] = id < a.V ? val(z, id) : 0ull;
+    tot += v[e];
+  }
+  const u64 inc = wave_incl_scan64(tot);
+  u64 m = inc - tot;
+  long long pick = -1;
+#pragma unroll
+  for (int e = 0; e < VL; ++e) {
+    if (m <= t && t < m + v[e]) pick = i0 + e;
+    m += v[e];
+  }
+  const u64 bal = __ballot(pick >= 0);
+  if (!bal) return -1;
+  const int src = __ffsll((long long)bal) - 1;
+  return (long long)readlane((u32)pick, src);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_solo(Args a) {
+  __shared__ SoloLds L;
+  constexpr int J = Chunk<DT>::J, VL = Chunk<DT>::VL;
+  const int row = (int)uni(a.order ? (u32)gld(a.order + blockIdx.x) : blockIdx.x);
+  if ((unsigned)row >= (unsigned)a.B) return;
+  const RowP p = row_params(a, row);
+  const int SH = a.SH;
+  const u64 thr = ceil_scaled(p.mp, 23 + SH);
+  if (p.pen) {
+    for (int i = threadIdx.x; i < min(p.hlen, kSoloHist); i += kThreads) L.hist[i] = gld(p.hist + i);
+    lds_sync();
+  }
+  // ---- pass 1: key range of q, or the greedy id
+  if (p.kind == kKindGreedy) {
+    u64 best = 0;
+    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < VL; ++e) {
+          const float z = elem_z(ch, p, L, c, j, e);
+          const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+          best = pk > best ? pk : best;
+        }
+    });
+    best = block_max64(best, L.s);
+    const u32 id = 0xffffffffu - (u32)best;
+    write_result(a, row, p, (long long)id, 0, 0, kPathGreedy, 0u, 0u, 0u, id, 1u);
+    return;
+  }
+  u32 kmax = 0, kmin = 0xffffffffu, nnan = 0;
+  u64 gbest = 0;
+  solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < VL; ++e) {
+        const float z = elem_z(ch, p, L, c, j, e);
+        const u32 k = ch.valid(j, e) ? skey(qdiv(z, p.T, p.rT, p.t_one)) : 0u;
+        kmax = max(kmax, k);
+        kmin = k ? min(kmin, k) : kmin;
+        nnan += k ? 1u : 0u;
+        const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+        gbest = pk > gbest ? pk : gbest;
+      }
+  });
+  {
+    u32 nk = ~kmin;
+    block_max2(kmax, nk, L.s);
+    kmin = ~nk;
+  }
+  gbest = block_max64(gbest, L.s);
+  nnan = block_sum(nnan, L.s);  // tokens whose q is not NaN
+  if (kmax == 0u) {  // every q is NaN: no weights, the greedy id (as the exact path)
+    write_result(a, row, p, (long long)(0xffffffffu - (u32)gbest), 0, thr, kPathSolo, 0u, 0u, 0u, 0u, 0u);
+    return;
+  }
+  const float qs = f_of_key(kmax);
+  // ---- top-k: the k-th largest key (ties kept), by key histograms
+  u32 kk = 1u;
+  if ((p.kind == kKindTopK || p.kind == kKindSingle) && nnan > (u32)p.k) {
+    u32 lo = kmin, hi = kmax;
+    u64 target = (u64)p.k;
+    for (int r = 0; r < 5; ++r) {
+      for (int b = threadIdx.x; b < kNB; b += kThreads) L.hc[b] = 0u;
+      lds_sync();
+      const int bl = bitlen(hi - lo);
+      const int sh = bl > 8 ? bl - 8 : 0;
+      solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int e = 0; e < VL; ++e) {
+            const u32 k = ch.valid(j, e) ? skey(qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one)) : 0u;
+            if (k >= lo && k <= hi && k) atomicAdd(&L.hc[(hi - k) >> sh], 1u);
+          }
+      });
+      lds_sync();
+      const int b = threadIdx.x;
+      const u32 bc = b < kNB ? L.hc[b] : 0u;
+      u32 tot;
+      const u32 ex = block_excl(bc, L.s, &tot);
+      if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
+      lds_sync();
+      if (b < kNB && (u64)ex < target && target <= (u64)ex + bc) {
+        L.s.r[12] = (u32)b;
+        L.s.r[13] = ex;
+      }
+      lds_sync();
+      const u32 bsel = uni(L.s.r[12]), exs = uni(L.s.r[13]);
+      lds_sync();
+      if (bsel == 0xffffffffu) break;  // cannot happen: nnan > k tokens lie in [kmin, kmax]
+      target -= exs;
+      const u32 nhi = hi - (bsel << sh);
+      const u32 span = (1u << sh) - 1u;
+      lo = (nhi - lo) > span ? nhi - span : lo;
+      hi = nhi;
+      if (sh == 0) {
+        kk = hi;
+        break;
+      }
+    }
+  }
+  auto wpk = [&](float q, u32 k) -> u32 {
+    const u32 x = (k >= kk && k) ? wpack_of(q, k, qs, kmax, SH) : 0u;
+    return wunpack(x) >= thr ? x : 0u;
+  };
+  const int nseg = a.G * kWaves * J;
+  // ---- pass 2: weights, S, per-segment masses, the first bracket histogram
+  Bracket br;
+  br.mb0 = mass_bins_first(qs - f_of_key(kmin));
+  br.lo = 0u;
+  br.hi = 0xffffffffu;
+  br.b0 = 0u;
+  for (int b = threadIdx.x; b < kNB; b += kThreads) L.mh[b] = 0ull;
+  lds_sync();
+  u64 S = 0;
+  u32 nz = 0;
+  solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      u64 sj = 0;
+#pragma unroll
+      for (int e = 0; e < VL; ++e) {
+        const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+        const u32 k = ch.valid(j, e) ? skey(q) : 0u;
+        const u32 x = wpk(q, k);
+        const u64 w = wunpack(x);
+        sj += w;
+        nz += x ? 1u : 0u;
+        if (p.topp && x) atomicAdd(&L.mh[mass_bin(q, k, qs, kmax, br.mb0)], w);
+      }
+      const u64 sw = wave_sum64(sj);
+      if (lane_id() == 0) L.seg[(c * kWaves + wave_id()) * J + j] = sw;
+      S += lane_id() == 0 ? sw : 0ull;
+    }
+  });
+  block_sum2(S, nz, L.s);
+  u64 W = S, A = 0, wt = 0;
+  u32 klo = kk, idlo = (u32)a.V, kept = nz;  // without top-p: K, the tokens with key >= kk
+  bool single = false;  // the bracket holds one key (too many tokens to list)
+  u32 jties = 0u;
+  if (p.topp) {
+    // ---- the bracket rounds
+    const u64 Tp = mul_frac(S, p.tp);
+    bool listed = false;
+    u32 rlo = 0u, rhi = 0u;  // key range binned by the next key-space round
+    for (int r = 0; r < kSoloRounds && !listed; ++r) {
+      if (r > 0) {
+        for (int b = threadIdx.x; b < kNB; b += kThreads) {
+          L.mh[b] = 0ull;
+          L.hc[b] = 0u;
+        }
+        lds_sync();
+        const u32 lo = rlo, hi = rhi;
+        const int bl = bitlen(hi - lo);
+        const int sh = bl > 8 ? bl - 8 : 0;
+        solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+          for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int e = 0; e < VL; ++e) {
+              const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+              const u32 k = ch.valid(j, e) ? skey(q) : 0u;
+              if (k && mass_bin(q, k, qs, kmax, br.mb0) == br.b0 && (k >= br.lo && k <= br.hi)) {
+                const u64 w = wunpack(wpk(q, k));
+                if (w) {
+                  const u32 b = key_bin(k, lo, hi, sh);
+                  atomicAdd(&L.mh[b], w);
+                  atomicAdd(&L.hc[b], 1u);
+                }
+              }
+            }
+        });
+        lds_sync();
+      }
+      // the crossing bin
+      const int b = threadIdx.x;
+      const u64 bm = b < kNB ? L.mh[b] : 0ull;
+      const u32 bc = (b < kNB && r > 0) ? L.hc[b] : 0u;
+      u64 tot;
+      const u64 ex = block_excl64(bm, L.s, &tot);
+      const u64 target = Tp - A;
+      if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
+      lds_sync();
+      if (b < kNB && ex <= target && target < ex + bm) {
+        L.s.r[12] = (u32)b;
+        L.s.r64[12] = ex;
+        u32 fits;
+        if (r == 0) {
+          const float wl = bin_least_weight(br.mb0, b, SH);
+          fits = (float)bm <= wl * (float)kSoloList ? 1u : 0u;
+        } else {
+          fits = bc <= (u32)kSoloList ? 1u : 0u;
+        }
+        L.s.r[13] = fits;
+        L.s.r[14] = bc;
+      }
+      lds_sync();
+      const u32 bsel = uni(L.s.r[12]), fits = uni(L.s.r[13]), bcount = uni(L.s.r[14]);
+      const u64 exs = uni64(L.s.r64[12]);
+      lds_sync();
+      if (bsel == 0xffffffffu) {  // cannot happen with exact sums: every row resolves below
+        write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
+        return;
+      }
+      A += exs;
+      if (r == 0) {
+        br.b0 = bsel;
+        // an estimate of the bin's key range (membership is decided by the bin)
+        const float xlo = bsel == 0u ? br.mb0.x0 : bin_edge(br.mb0, bsel - 1u);
+        const float xhi = bin_edge(br.mb0, bsel);
+        const u32 khi = skey(qs - fmaxf(xlo * 0.999f - 1e-6f, 0.0f));
+        const u32 klw = skey(qs - (xhi * 1.001f + 1e-6f));
+        br.hi = 0xffffffffu;  // the bracket: every key of bin b0
+        br.lo = 0u;
+        rhi = min(kmax, khi);
+        rlo = min(max(kmin, klw), rhi);
+      } else {
+        const int bl = bitlen(rhi - rlo);
+        const int sh = bl > 8 ? bl - 8 : 0;
+        const u32 nhi = rhi - (bsel << sh);
+        const u32 span = (1u << sh) - 1u;
+        const u32 nlo = (nhi - rlo) > span ? nhi - span : rlo;
+        // the first and last bins also hold the bin-b0 keys past the binned range
+        if (bsel != 0u) br.hi = min(br.hi, nhi);
+        if (bsel != (u32)kNB - 1u) br.lo = max(br.lo, nlo);
+        rhi = min(br.hi, kmax);
+        rlo = min(max(br.lo, kmin), rhi);
+        if (max(br.lo, kmin) == min(br.hi, kmax) && !fits) {
+          single = true;  // one key, too many tokens to list
+          jties = bcount;
+          break;
+        }
+      }
+      listed = fits != 0u;
+    }
+    if (!listed && !single) {  // a bracket still too wide after every round: cannot happen for 32-bit keys
+      write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
+      return;
+    }
+    // ---- pass 3: the bracket's tokens listed, the mass above it per segment
+    if (threadIdx.x == 0) L.nlist = 0u;
+    for (int i = threadIdx.x; i < nseg; i += kThreads) L.segt[i] = 0u;
+    lds_sync();
+    u32 nzb = 0;  // tokens at or below the bracket with nonzero weight
+    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        u64 sub = 0;
+        u32 ties = 0;
+#pragma unroll
+        for (int e = 0; e < VL; ++e) {
+          const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+          const u32 k = ch.valid(j, e) ? skey(q) : 0u;
+          if (!k) continue;
+          const int side = bracket_side(br, q, k, qs, kmax);
+          if (side == 0) continue;
+          const u64 w = wunpack(wpk(q, k));
+          sub += w;
+          nzb += w ? 1u : 0u;
+          if (side == 1 && w) {
+            if (single) {
+              ++ties;
+            } else {
+              const u32 slot = atomicAdd(&L.nlist, 1u);
+              if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)ch.id(j, e);
+            }
+          }
+        }
+        const u64 sw = wave_sum64(sub);
+        const u32 tw = wave_sum(ties);
+        if (lane_id() == 0) {
+          const int sg = (c * kWaves + wave_id()) * J + j;
+          L.seg[sg] -= sw;
+          L.segt[sg] = tw;
+        }
+      }
+    });
+    nzb = block_sum(nzb, L.s);
+    const u32 na = nz - nzb;  // tokens above the bracket with nonzero weight
+    if (!single) {
+      const u32 n = uni(L.nlist);
+      if (n > (u32)kSoloList || n == 0u) {  // the bound was exceeded: cannot happen
+        write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStOverflow, kmax, 0u, 0u, 0u);
+        return;
+      }
+      Held h;
+      hold_entries(L, n, h);
+      u32 wq[kFPer];
+#pragma unroll
+      for (int i = 0; i < kFPer; ++i) {
+        const u32 k = (u32)(h.e[i] >> 32);
+        wq[i] = ((u32)i < h.per && k) ? wpk(f_of_key(k), k) : 0u;
+      }
+      const SelRes q = held_select<true>(a, L, h, wq, max(max(br.lo, kmin), 1u), min(br.hi, kmax), Tp - A);
+      if (!q.ok) {
+        write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
+        return;
+      }
+      klo = q.kappa;
+      wt = wunpack(wpk(f_of_key(klo), klo));
+      const u64 jj = div_small(Tp - A - q.mass_above, wt) + 1ull;
+      jties = (u32)(jj < (u64)q.cnt_at ? jj : (u64)q.cnt_at);
+      W = A + q.mass_above + (u64)jties * wt;
+      kept = na + q.cnt_above + jties;
+      idlo = (u32)a.V;
+      if (jties < q.cnt_at) {
+        // the jties-th tie in id order: the jties-th largest of ~id among the ties
+        Held t;
+        t.per = h.per;
+#pragma unroll
+        for (int i = 0; i < kFPer; ++i) {
+          const u32 k = (u32)(h.e[i] >> 32), id = (u32)h.e[i];
+          t.e[i] = (wq[i] && k == klo) ? (((u64)(~id) << 32) | id) : 0ull;
+        }
+        const SelRes r = held_select<false>(a, L, t, wq, ~(u32)(a.V - 1), 0xffffffffu, (u64)jties);
+        if (!r.ok) {
+          write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
+          return;
+        }
+        idlo = ~r.kappa;
+      }
+      // kept mass per segment: above the bracket, plus the listed tokens kept
+#pragma unroll
+      for (int i = 0; i < kFPer; ++i) {
+        if ((u32)i < h.per && wq[i]) {
+          const u32 k = (u32)(h.e[i] >> 32), id = (u32)h.e[i];
+          if (k > klo || (k == klo && id <= idlo)) atomicAdd(&L.seg[seg_of<DT>((int)id)], wunpack(wq[i]));
+        }
+      }
+      lds_sync();
+    } else {
+      // a bracket of one key: every token in it weighs wt; the first jties in id order are kept
+      klo = min(br.hi, kmax);
+      wt = wunpack(wpk(f_of_key(klo), klo));
+      const u32 cnt_at = jties;
+      const u64 jj = div_small(Tp - A, wt) + 1ull;
+      jties = (u32)(jj < (u64)cnt_at ? jj : (u64)cnt_at);
+      W = A + (u64)jties * wt;
+      kept = na + jties;
+      idlo = (u32)a.V;
+      if (jties < cnt_at) {
+        // the segment holding the jties-th tie, then its id from one wave's re-read
+        u32 c0 = threadIdx.x * 2 < (u32)nseg ? L.segt[threadIdx.x * 2] : 0u;
+        u32 c1 = threadIdx.x * 2 + 1 < (u32)nseg ? L.segt[threadIdx.x * 2 + 1] : 0u;
+        u32 ctot;
+        const u32 cx = block_excl(c0 + c1, L.s, &ctot);
+        if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
+        lds_sync();
+        const u32 jt = jties - 1u;  // ties before the wanted one
+        if (cx <= jt && jt < cx + c0) {
+          L.s.r[12] = threadIdx.x * 2;
+          L.s.r[13] = jt - cx;
+        } else if (cx + c0 <= jt && jt < cx + c0 + c1) {
+          L.s.r[12] = threadIdx.x * 2 + 1;
+          L.s.r[13] = jt - cx - c0;
+        }
+        lds_sync();
+        const u32 sg = uni(L.s.r[12]), within = uni(L.s.r[13]);
+        lds_sync();
+        if (sg == 0xffffffffu) {
+          write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
+          return;
+        }
+        if (p.pen) pen_build(p, (int)sg / (kWaves * J), L);
+        if (threadIdx.x < 64) {
+          const long long id = seg_find<DT>(a, p, row, L, (int)sg, (u64)within, [&](float z, int) -> u64 {
+            const float q = qdiv(z, p.T, p.rT, p.t_one);
+            const u32 k = skey(q);
+            return (k == klo && wpk(q, k)) ? 1ull : 0ull;
+          });
+          if (threadIdx.x == 0) L.s.r[15] = (u32)id;
+        }
+        lds_sync();
+        idlo = L.s.r[15];
+        lds_sync();
+      }
+      // kept mass per segment: above, plus the ties up to the jties-th
+      // ties before segment s in id order (exclusive), capped at jties
+      {
+        const u32 s0 = threadIdx.x * 2, s1 = s0 + 1;
+        u32 c0 = s0 < (u32)nseg ? L.segt[s0] : 0u;
+        u32 c1 = s1 < (u32)nseg ? L.segt[s1] : 0u;
+        u32 ctot;
+        const u32 cx = block_excl(c0 + c1, L.s, &ctot);
+        const u32 k0 = min(c0, jties > cx ? jties - cx : 0u);
+        const u32 cx1 = cx + c0;
+        const u32 k1 = min(c1, jties > cx1 ? jties - cx1 : 0u);
+        if (s0 < (u32)nseg) L.seg[s0] += (u64)k0 * wt;
+        if (s1 < (u32)nseg) L.seg[s1] += (u64)k1 * wt;
+      }
+      lds_sync();
+    }
+  }
+  // ---- the draw: the segment holding t, then the token inside it
+  const u64 t = mul_frac(W, p.u);
+  {
+    const u32 s0 = threadIdx.x * 2, s1 = s0 + 1;
+    const u64 m0 = s0 < (u32)nseg ? L.seg[s0] : 0ull, m1 = s1 < (u32)nseg ? L.seg[s1] : 0ull;
+    u64 mt;
+    const u64 mx = block_excl64(m0 + m1, L.s, &mt);
+    if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
+    lds_sync();
+    if (mx <= t && t < mx + m0) {
+      L.s.r[12] = s0;
+      L.s.r64[12] = t - mx;
+    } else if (mx + m0 <= t && t < mx + m0 + m1) {
+      L.s.r[12] = s1;
+      L.s.r64[12] = t - mx - m0;
+    }
+    lds_sync();
+  }
+  const u32 sg = uni(L.s.r[12]);
+  const u64 tin = uni64(L.s.r64[12]);
+  lds_sync();
+  if (sg == 0xffffffffu) {
+    write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStIncomplete, kmax, 0u, 0u, 0u);
+    return;
+  }
+  if (p.pen) pen_build(p, (int)sg / (kWaves * J), L);
+  if (threadIdx.x < 64) {
+    const bool topp = p.topp;
+    const long long id = seg_find<DT>(a, p, row, L, (int)sg, tin, [&](float z, int i) -> u64 {
+      const float q = qdiv(z, p.T, p.rT, p.t_one);
+      const u32 k = skey(q);
+      const u64 w = wunpack(wpk(q, k));
+      if (!topp) return w;
+      return (k > klo || (k == klo && (u32)i <= idlo)) ? w : 0ull;
+    });
+    if (threadIdx.x == 0) L.s.r[15] = (u32)(id < 0 ? 0xffffffffu : (u32)id);
+  }
+  lds_sync();
+  const u32 pick = L.s.r[15];
+  write_result(a, row, p, pick == 0xffffffffu ? -1ll : (long long)pick, W, thr, kPathSolo,
+               pick == 0xffffffffu ? kStIncomplete : 0u, kmax, klo, idlo, kept);
+}
+
+}  // namespace qs

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include "qs_kernels.hpp"
+#include "qs_solo.hpp"
 #include "qs_step.hpp"
 #include "qsampler.h"
 
@@ -141,7 +142,7 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   if (H < 0 || H > QS_MAX_HISTORY) return fail("qs_sample: history length out of range (%lld)", H);
   if ((H > 0) != (hist_ids != nullptr)) return fail("qs_sample: hist_ids and H must be given together");
   if (hist_len && !hist_ids) return fail("qs_sample: hist_len needs hist_ids");
-  if (flags & ~(QS_FLAG_ALL_GREEDY | QS_FLAG_USE_TOP_P | QS_FLAG_NO_WAIT))
+  if (flags & ~(QS_FLAG_ALL_GREEDY | QS_FLAG_USE_TOP_P | QS_FLAG_NO_WAIT | QS_FLAG_SOLO))
     return fail("qs_sample: unknown flags 0x%llx", flags);
   Layout L;
   if (!layout_for(B, V, &L)) return fail("qs_sample: V too large (%lld)", V);
@@ -187,10 +188,18 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   a.trace = (u64*)g_trace;
 #endif
   const dim3 grid(L.G, B), block(kThreads);
-  if (logits_dtype == QS_DTYPE_F32)
+  const int J = logits_dtype == QS_DTYPE_F32 ? 4 : 2;  // 16-byte vectors per thread and chunk
+  const bool solo = (flags & QS_FLAG_SOLO) && L.G * kWaves * J <= kSoloSegs;
+  if (solo) {
+    if (logits_dtype == QS_DTYPE_F32)
+      hipLaunchKernelGGL(k_solo<QS_DTYPE_F32>, dim3(B), block, 0, stream, a);
+    else
+      hipLaunchKernelGGL(k_solo<QS_DTYPE_BF16>, dim3(B), block, 0, stream, a);
+  } else if (logits_dtype == QS_DTYPE_F32) {
     hipLaunchKernelGGL(k_sample<QS_DTYPE_F32>, grid, block, 0, stream, a);
-  else
+  } else {
     hipLaunchKernelGGL(k_sample<QS_DTYPE_BF16>, grid, block, 0, stream, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail("qs_sample: launch failed (%lld)", (long long)e);
   if (out_probs) {

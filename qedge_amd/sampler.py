@@ -16,6 +16,9 @@ from torch import nn
 from . import _lib
 
 _DTYPES = {torch.float32: _lib.QS_DTYPE_F32, torch.bfloat16: _lib.QS_DTYPE_BF16}
+# From this many rows (and no top-k), one workgroup per row beats cooperating
+# workgroups: the batch alone fills the GPU.
+SOLO_MIN_ROWS = 512
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -63,11 +66,13 @@ def sample_into(logits: torch.Tensor, out_ids: torch.Tensor, workspace: Workspac
                 history_len: torch.Tensor | None = None, uniforms: torch.Tensor | None = None,
                 row_order: torch.Tensor | None = None, all_greedy: bool = False, use_top_p: bool = False,
                 out_probs: torch.Tensor | None = None, out_kept: torch.Tensor | None = None,
-                no_wait: bool = False) -> torch.Tensor:
+                no_wait: bool = False, solo: bool | None = None) -> torch.Tensor:
     """Sample into caller-owned ``out_ids`` (int64 [B]); allocates nothing.
 
     Every tensor must be on the logits' device; sizes and dtypes are checked
     here (ValueError) so that no kernel reads or writes outside a buffer.
+    ``solo`` resolves every row by one workgroup (QS_FLAG_SOLO); by default it
+    is used for batches of at least SOLO_MIN_ROWS rows without top-k.
     """
     if logits.dim() != 2 or logits.dtype not in _DTYPES or not logits.is_cuda:
         raise ValueError("logits must be a [B, V] float32/bfloat16 device tensor")
@@ -102,8 +107,10 @@ def sample_into(logits: torch.Tensor, out_ids: torch.Tensor, workspace: Workspac
         if (out_probs.dtype != torch.float32 or out_probs.dim() != 2 or out_probs.shape[0] < B
                 or out_probs.shape[1] != V or not out_probs.is_contiguous() or out_probs.device != dev):
             raise ValueError("out_probs must be a contiguous float32 [>= B, V] tensor on the logits' device")
+    if solo is None:
+        solo = B >= SOLO_MIN_ROWS and top_ks is None
     flags = ((_lib.QS_FLAG_ALL_GREEDY if all_greedy else 0) | (_lib.QS_FLAG_USE_TOP_P if use_top_p else 0)
-             | (_lib.QS_FLAG_NO_WAIT if no_wait else 0))
+             | (_lib.QS_FLAG_NO_WAIT if no_wait else 0) | (_lib.QS_FLAG_SOLO if solo else 0))
     f32, i32 = torch.float32, torch.int32
     args = (
         ctypes.c_void_p(logits.data_ptr()), logits.stride(0), _DTYPES[logits.dtype], B, V,
