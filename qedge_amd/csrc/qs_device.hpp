@@ -365,6 +365,26 @@ __device__ __forceinline__ u64 ceil_scaled(float f, int e) {
   if (sh >= 64) return 1;
   return (m >> sh) + ((m & ((1ull << sh) - 1ull)) != 0ull);
 }
+// The least packed weight (as wpack_of makes them) whose weight is >= thr, so
+// that w >= thr can be tested on packed weights: packed weights are ordered as
+// their weights.  0 for thr == 0; 0xffffffff when no weight reaches thr.
+__device__ __forceinline__ u32 packed_threshold(u64 thr) {
+  if (thr == 0ull) return 0u;
+  for (int s = -23; s < 64; ++s) {
+    const u32 top = (u32)(s + 64) << 24;
+    if (wunpack(top | 0xffffffu) < thr) continue;
+    u32 lo = 0x800000u, hi = 0xffffffu;  // the least mantissa M with unpack >= thr
+    while (lo < hi) {
+      const u32 mid = (lo + hi) >> 1;
+      if (wunpack(top | mid) >= thr)
+        hi = mid;
+      else
+        lo = mid + 1u;
+    }
+    return top | lo;
+  }
+  return 0xffffffffu;
+}
 // Values equal in every lane, moved to scalar registers.
 __device__ __forceinline__ u32 uni(u32 v) { return (u32)__builtin_amdgcn_readfirstlane((int)v); }
 __device__ __forceinline__ u64 uni64(u64 v) { return ((u64)uni((u32)(v >> 32)) << 32) | uni((u32)v); }

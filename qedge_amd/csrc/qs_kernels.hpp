@@ -37,7 +37,7 @@ constexpr int kNB = 256;                   // mass histogram bins (one per threa
 constexpr int kRounds = 3;                 // bracket rounds before the exact path
 constexpr int kLC = 256;                   // bracket entries per chunk
 constexpr int kNBS = 1024;                 // select histogram bins
-constexpr int kStageCap = 1024;            // entries staged in LDS by one workgroup
+constexpr int kRegionCap = 1024;           // candidate entries of one chunk at most
 
 enum : u32 { kStOverflow = 1u, kStIncomplete = 2u, kStTimeout = 4u, kStList = 8u };
 constexpr u32 kWhyLargeK = 16u;          // top-k above kTopkMax
@@ -174,7 +174,6 @@ struct Lds {
   union {
     u32 pen[kCH / 2];       // history counts of the chunk, two 16-bit counts per word
     u32 kq[kCH];            // top-k-off rows: keys of q, element i of thread t at i * kThreads + t
-    u64 stage[kStageCap];   // entries staged for a region
     FinLds fin;             // the finishing workgroup's candidates
   } u;
   SelLds sel;               // select histogram (beside the table: the exact pass needs both)
@@ -257,6 +256,28 @@ __device__ __forceinline__ void pen_build(const RowP& p, int c, LT& L) {
   const int lo = c * kCH;
   for (int i = threadIdx.x; i < p.hlen; i += kThreads) {
     const int d = hist_id(p, L, i) - lo;
+    if ((unsigned)d < (unsigned)kCH) atomicAdd(&t[d >> 1], (d & 1) ? 0x10000u : 1u);
+  }
+  lds_sync();
+}
+// The same with the first kHistPre * kThreads history ids already loaded (pre[i]
+// is id threadIdx.x + i * kThreads, loaded beside the chunk so that the table
+// costs no further round trip).
+constexpr int kHistPre = 8;
+__device__ __forceinline__ void pen_build_pre(const RowP& p, int c, Lds& L, const int (&pre)[kHistPre]) {
+  u32* t = pen_table(L);
+  uint4* t4 = (uint4*)t;
+  for (int i = threadIdx.x; i < kCH / 8; i += kThreads) t4[i] = make_uint4(0u, 0u, 0u, 0u);
+  lds_sync();
+  const int lo = c * kCH;
+#pragma unroll
+  for (int k = 0; k < kHistPre; ++k) {
+    const int i = (int)threadIdx.x + k * kThreads;
+    const int d = pre[k] - lo;
+    if (i < p.hlen && (unsigned)d < (unsigned)kCH) atomicAdd(&t[d >> 1], (d & 1) ? 0x10000u : 1u);
+  }
+  for (int i = threadIdx.x + kHistPre * kThreads; i < p.hlen; i += kThreads) {
+    const int d = gld(p.hist + i) - lo;
     if ((unsigned)d < (unsigned)kCH) atomicAdd(&t[d >> 1], (d & 1) ? 0x10000u : 1u);
   }
   lds_sync();
@@ -1314,47 +1335,54 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
   tau = max(tau, 1u);
   QS_TR(3);
   const int R = a.R;
-  u32 n = 0;
+  u32 n = 0, below = 0, zmax = 0;
+  u64* reg = row_data(a, row) + (size_t)c * R;
   for (int attempt = 0; attempt < 2; ++attempt) {
-    // positions in id order: (wave, j, lane, e)
-    u32 cnt[J];
-    u32 tot = 0;
+    // positions in id order (wave, j, lane, e), the largest key left out and the
+    // chunk's largest, with one exchange
+    u32 cnt[J], ex[J], tj[J];
+    u32 bl = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       u32 x = 0;
 #pragma unroll
-      for (int e = 0; e < VL; ++e) x += kz[j * VL + e] >= tau ? 1u : 0u;
+      for (int e = 0; e < VL; ++e) {
+        const u32 kx = kz[j * VL + e];
+        x += kx >= tau ? 1u : 0u;
+        bl = kx < tau ? max(bl, kx) : bl;
+      }
       cnt[j] = x;
     }
-    u32 ex[J];
+    u32 tot = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const u32 inc = wave_incl_scan(cnt[j]);
       ex[j] = inc - cnt[j];
-      const u32 tj = readlane(inc, 63);
-      L.s.v[wave_id()][j] = tj;  // same value from every lane
-      tot += tj;
+      tj[j] = readlane(inc, 63);
+      tot += tj[j];
     }
-    if (lane_id() == 0) L.s.r[wave_id()] = tot;
+    bl = wave_max(bl);
+    const u32 wm = wave_max(m);
+    if (lane_id() == 0) {
+      L.s.r[wave_id()] = tot;
+      L.s.v[wave_id()][5] = bl;
+      L.s.v[wave_id()][6] = wm;
+    }
     lds_sync();
     u32 woff = 0;
     n = 0;
+    below = 0;
+    zmax = 0;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) {
-      woff += i < wave_id() ? L.s.r[i] : 0u;
-      n += L.s.r[i];
+      const u32 ti = L.s.r[i];
+      woff += i < wave_id() ? ti : 0u;
+      n += ti;
+      below = max(below, L.s.v[i][5]);
+      zmax = max(zmax, L.s.v[i][6]);
     }
-    u32 joff[J];
-    {
-      u32 run = woff;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        joff[j] = run;
-        run += L.s.v[wave_id()][j];
-      }
-    }
-    lds_sync();
-    if (n > (u32)R || n > (u32)kStageCap) {
+    if (n > (u32)R) {
+      lds_sync();  // the exchange is read: it may be written again
       if (attempt == 0) {
         tau = tau + 1u;  // ties at tau overflowed the region: strictly above it
         continue;
@@ -1362,34 +1390,26 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
       n = 0xffffffffu;
       break;
     }
-    // stage (local index, z key) in id order, then one entry per thread
+    // each candidate straight to the region, as (key of q << 32 | id)
+    u32 run = woff;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      u32 pos = joff[j] + ex[j];
+      u32 pos = run + ex[j];
 #pragma unroll
       for (int e = 0; e < VL; ++e) {
         const u32 kx = kz[j * VL + e];
         if (kx >= tau) {
-          L.u.stage[pos] = ((u64)kx << 32) | (u32)ch.id(j, e);
+          const float q = qdiv(f_of_key(kx), p.T, p.rT, p.t_one);
+          stc(&reg[pos], ((u64)skey(q) << 32) | (u32)ch.id(j, e));
           ++pos;
         }
       }
-    }
-    lds_sync();
-    u64* reg = row_data(a, row) + (size_t)c * R;
-    for (u32 i = threadIdx.x; i < n; i += kThreads) {
-      const u64 st = L.u.stage[i];
-      const float q = qdiv(f_of_key((u32)(st >> 32)), p.T, p.rT, p.t_one);
-      stc(&reg[i], ((u64)skey(q) << 32) | (u32)st);
+      run += tj[j];
     }
     QS_TR(4);
     break;
   }
-  // largest z key left out, and the chunk's largest; the q keys of the latter and of tau
-  u32 below = 0, zmax = m;
-#pragma unroll
-  for (int i = 0; i < E; ++i) below = kz[i] < tau ? max(below, kz[i]) : below;
-  block_max2(below, zmax, L.s);
+  // the q keys of the chunk's largest and of tau
   if (threadIdx.x == 0) {
     const u32 qmax = zmax ? skey(qdiv(f_of_key(zmax), p.T, p.rT, p.t_one)) : 0u;
     const u32 qlow = skey(qdiv(f_of_key(tau), p.T, p.rT, p.t_one));
@@ -1467,6 +1487,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   }
   const int SH = a.SH;
   const u64 thr = ceil_scaled(p.mp, 23 + SH);
+  const u32 pthr = uni(packed_threshold(thr));
   const float qs = f_of_key(kstar);
   // first-round bins over x = q* - q in [0, D], D = min(q* - q_min, kXMax)
   MassBins mb = mass_bins_first(qs - f_of_key(kmin));
@@ -1489,8 +1510,8 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       const u32 k = L.u.kq[i * kThreads + threadIdx.x];
       const float q = f_of_key(k);
       u32 x = wpack_of(q, k, qs, kstar, SH);
+      x = x >= pthr ? x : 0u;
       const u64 w = wunpack(x);
-      x = w >= thr ? x : 0u;
       wp[i] = x;
       Sc += x ? w : 0ull;
       nz += x ? 1u : 0u;
@@ -1834,10 +1855,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   QS_TR(0);
   Chunk<DT> ch;
   load_chunk<DT>(a, row, c, ch);
+  int pre[kHistPre];  // the row's first history ids, loaded beside the chunk
+  if (a.hist) {
+    const int* h = a.hist + (size_t)row * a.H;
+#pragma unroll
+    for (int k = 0; k < kHistPre; ++k) {
+      const int i = (int)threadIdx.x + k * kThreads;
+      pre[k] = i < a.H ? gld(h + i) : -1;
+    }
+  }
   const RowP p = row_params(a, row);
   RowSync* sy = &a.sync[row];
   Slot* sl = row_slots(a, row);
-  if (p.pen) pen_build(p, c, L);
+  if (p.pen) pen_build_pre(p, c, L, pre);
   QS_TR(1);
   (void)E;
   (void)J;

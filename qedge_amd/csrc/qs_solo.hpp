@@ -164,6 +164,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   const RowP p = row_params(a, row);
   const int SH = a.SH;
   const u64 thr = ceil_scaled(p.mp, 23 + SH);
+  const u32 pthr = uni(packed_threshold(thr));
   if (p.pen) {
     for (int i = threadIdx.x; i < min(p.hlen, kSoloHist); i += kThreads) L.hist[i] = gld(p.hist + i);
     lds_sync();
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   }
   auto wpk = [&](float q, u32 k) -> u32 {
     const u32 x = (k >= kk && k) ? wpack_of(q, k, qs, kmax, SH) : 0u;
-    return wunpack(x) >= thr ? x : 0u;
+    return x >= pthr ? x : 0u;
   };
   const int nseg = a.G * kWaves * J;
   // ---- pass 2: weights, S, per-segment masses, the first bracket histogram

@@ -49,7 +49,7 @@ bool layout_for(int B, int V, Layout* L) {
   L->G = (V + kCH - 1) / kCH;
   if (L->G > kMaxG) return false;
   L->R = kRegionTotal / L->G;
-  if (L->R > kStageCap) L->R = kStageCap;
+  if (L->R > kRegionCap) L->R = kRegionCap;
   L->SH = shift_of(V);
   const long long cand = (long long)L->G * L->R;
   const long long mass = (long long)kRounds * kNB + (long long)L->G * kLC;
