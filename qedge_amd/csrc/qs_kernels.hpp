@@ -223,7 +223,9 @@ __device__ __forceinline__ void load_chunk(const Args& a, int row, int c, Chunk<
       else
         ch.v[j] = gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
     } else {
-      u32 x[4] = {0u, 0u, 0u, 0u};
+      // past V: NaN, whose key of q is 0 (no weight, never a candidate)
+      const u32 pad = DT == QS_DTYPE_F32 ? 0x7fc00000u : 0x7fc07fc0u;
+      u32 x[4] = {pad, pad, pad, pad};
       if (DT == QS_DTYPE_F32) {
         const float* p = (const float*)a.logits + rowoff;
 #pragma unroll
@@ -233,7 +235,8 @@ __device__ __forceinline__ void load_chunk(const Args& a, int row, int c, Chunk<
         const uint16_t* p = (const uint16_t*)a.logits + rowoff;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (i0 + e < a.V) x[e >> 1] |= (u32)gld(p + i0 + e) << ((e & 1) * 16);
+          if (i0 + e < a.V)
+            x[e >> 1] = (x[e >> 1] & ~(0xffffu << ((e & 1) * 16))) | ((u32)gld(p + i0 + e) << ((e & 1) * 16));
       }
       ch.v[j] = make_uint4(x[0], x[1], x[2], x[3]);
     }
@@ -306,7 +309,7 @@ __device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, 
 #pragma unroll
     for (int e = 0; e < Chunk<DT>::VL; ++e) {
       const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
-      kq[j * Chunk<DT>::VL + e] = ch.valid(j, e) ? skey(q) : 0u;
+      kq[j * Chunk<DT>::VL + e] = skey(q);  // 0 past V (NaN padding)
     }
 }
 
@@ -1286,7 +1289,7 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
   for (int j = 0; j < J; ++j)
 #pragma unroll
     for (int e = 0; e < VL; ++e) {
-      const u32 kx = ch.valid(j, e) ? skey(elem_z(ch, p, L, c, j, e)) : 0u;
+      const u32 kx = skey(elem_z(ch, p, L, c, j, e));  // 0 past V (NaN padding)
       kz[j * VL + e] = kx;
       m = max(m, kx);
     }

@@ -78,10 +78,9 @@ __device__ __forceinline__ void solo_pass(const Args& a, const RowP& p, int row,
   }
 }
 
-// The bracket: tokens with mass_bin(q; mb0) == b0 and key in [lo, hi].  The
-// key bounds start as an estimate of bin b0's key range; the key-space rounds
-// put the tokens of bin b0 outside [lo, hi] in their first or last bin, so
-// every token of bin b0 is accounted for whatever the estimate.
+// The bracket: the tokens with key in [lo, hi].  After the first round it is
+// mass bin b0's exact key range (mass_bin falls as the key grows); each
+// key-space round narrows it to one of its 256 key bins.
 struct Bracket {
   MassBins mb0;
   u32 b0, lo, hi;
@@ -90,10 +89,8 @@ struct Bracket {
 __device__ __forceinline__ u32 key_bin(u32 k, u32 lo, u32 hi, int sh) {
   return k > hi ? 0u : (k < lo ? (u32)kNB - 1u : (hi - k) >> sh);
 }
-// 0: above the bracket, 1: in it, 2: below it.
-__device__ __forceinline__ int bracket_side(const Bracket& br, float q, u32 k, float qs, u32 ks) {
-  const u32 b = mass_bin(q, k, qs, ks, br.mb0);
-  if (b != br.b0) return b < br.b0 ? 0 : 2;
+// 0: above the bracket, 1: in it, 2: below it (the bracket is the key range [lo, hi]).
+__device__ __forceinline__ int bracket_side(const Bracket& br, u32 k) {
   return k > br.hi ? 0 : (k < br.lo ? 2 : 1);
 }
 
@@ -189,27 +186,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   }
   u32 kmax = 0, kmin = 0xffffffffu, nnan = 0;
   u64 gbest = 0;
-  solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+  if (!p.pen) {
+    // z is the logit: q* and q_min are the quotients of its maximum and minimum
+    // (z / T is monotone), which NaN-ignoring max / min find; NaN past V
+    float zmx = -__builtin_inff(), zmn = __builtin_inff();
+    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+      (void)c;
 #pragma unroll
-    for (int j = 0; j < J; ++j)
+      for (int j = 0; j < J; ++j)
 #pragma unroll
-      for (int e = 0; e < VL; ++e) {
-        const float z = elem_z(ch, p, L, c, j, e);
-        const u32 k = ch.valid(j, e) ? skey(qdiv(z, p.T, p.rT, p.t_one)) : 0u;
-        kmax = max(kmax, k);
-        kmin = k ? min(kmin, k) : kmin;
-        nnan += k ? 1u : 0u;
-        const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
-        gbest = pk > gbest ? pk : gbest;
-      }
-  });
-  {
+        for (int e = 0; e < VL; ++e) {
+          const float z = ch.raw(j, e);
+          zmx = fmaxf(zmx, z);
+          zmn = fminf(zmn, z);
+          nnan += z == z ? 1u : 0u;
+        }
+    });
+    u32 kx = skey(zmx), kn = ~skey(zmn);
+    block_max2(kx, kn, L.s);
+    nnan = block_sum(nnan, L.s);
+    if (nnan) {
+      kmax = skey(qdiv(f_of_key(kx), p.T, p.rT, p.t_one));
+      kmin = skey(qdiv(f_of_key(~kn), p.T, p.rT, p.t_one));
+    }
+    gbest = 0xffffffffu;  // every z NaN: the first id
+  } else {
+    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < VL; ++e) {
+          const float z = elem_z(ch, p, L, c, j, e);
+          const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));  // 0 past V (NaN padding)
+          kmax = max(kmax, k);
+          kmin = k ? min(kmin, k) : kmin;
+          nnan += k ? 1u : 0u;
+          const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+          gbest = pk > gbest ? pk : gbest;
+        }
+    });
     u32 nk = ~kmin;
     block_max2(kmax, nk, L.s);
     kmin = ~nk;
+    gbest = block_max64(gbest, L.s);
+    nnan = block_sum(nnan, L.s);  // tokens whose q is not NaN
   }
-  gbest = block_max64(gbest, L.s);
-  nnan = block_sum(nnan, L.s);  // tokens whose q is not NaN
   if (kmax == 0u) {  // every q is NaN: no weights, the greedy id (as the exact path)
     write_result(a, row, p, (long long)(0xffffffffu - (u32)gbest), 0, thr, kPathSolo, 0u, 0u, 0u, 0u, 0u);
     return;
@@ -230,7 +251,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         for (int j = 0; j < J; ++j)
 #pragma unroll
           for (int e = 0; e < VL; ++e) {
-            const u32 k = ch.valid(j, e) ? skey(qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one)) : 0u;
+            const u32 k = skey(qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one));
             if (k >= lo && k <= hi && k) atomicAdd(&L.hc[(hi - k) >> sh], 1u);
           }
       });
@@ -282,7 +303,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
       for (int e = 0; e < VL; ++e) {
         const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
-        const u32 k = ch.valid(j, e) ? skey(q) : 0u;
+        const u32 k = skey(q);
         const u32 x = wpk(q, k);
         const u64 w = wunpack(x);
         sj += w;
@@ -320,8 +341,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
             for (int e = 0; e < VL; ++e) {
               const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
-              const u32 k = ch.valid(j, e) ? skey(q) : 0u;
-              if (k && mass_bin(q, k, qs, kmax, br.mb0) == br.b0 && (k >= br.lo && k <= br.hi)) {
+              const u32 k = skey(q);
+              if (k && k >= br.lo && k <= br.hi) {
                 const u64 w = wunpack(wpk(q, k));
                 if (w) {
                   const u32 b = key_bin(k, lo, hi, sh);
@@ -366,15 +387,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       A += exs;
       if (r == 0) {
         br.b0 = bsel;
-        // an estimate of the bin's key range (membership is decided by the bin)
-        const float xlo = bsel == 0u ? br.mb0.x0 : bin_edge(br.mb0, bsel - 1u);
-        const float xhi = bin_edge(br.mb0, bsel);
-        const u32 khi = skey(qs - fmaxf(xlo * 0.999f - 1e-6f, 0.0f));
-        const u32 klw = skey(qs - (xhi * 1.001f + 1e-6f));
-        br.hi = 0xffffffffu;  // the bracket: every key of bin b0
-        br.lo = 0u;
-        rhi = min(kmax, khi);
-        rlo = min(max(kmin, klw), rhi);
+        // the bin's exact key range: mass_bin falls as the key grows
+        auto bin = [&](u32 k) { return mass_bin(f_of_key(k), k, qs, kmax, br.mb0); };
+        u32 lo = kmin, hi = kmax;  // the largest key whose bin is >= bsel
+        while (lo < hi) {
+          const u32 mid = lo + (hi - lo + 1u) / 2u;
+          if (bin(mid) >= bsel) lo = mid; else hi = mid - 1u;
+        }
+        br.hi = lo;
+        lo = kmin;
+        hi = kmax;  // the least key whose bin is <= bsel
+        while (lo < hi) {
+          const u32 mid = lo + (hi - lo) / 2u;
+          if (bin(mid) <= bsel) hi = mid; else lo = mid + 1u;
+        }
+        br.lo = lo;
+        rhi = br.hi;
+        rlo = min(br.lo, rhi);
       } else {
         const int bl = bitlen(rhi - rlo);
         const int sh = bl > 8 ? bl - 8 : 0;
@@ -411,9 +440,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
         for (int e = 0; e < VL; ++e) {
           const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
-          const u32 k = ch.valid(j, e) ? skey(q) : 0u;
+          const u32 k = skey(q);
           if (!k) continue;
-          const int side = bracket_side(br, q, k, qs, kmax);
+          const int side = bracket_side(br, k);
           if (side == 0) continue;
           const u64 w = wunpack(wpk(q, k));
           sub += w;
