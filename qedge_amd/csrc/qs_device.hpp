@@ -287,8 +287,9 @@ __device__ __forceinline__ float qdiv(float z, float T, float rT, bool t_one) {
   if (t_one) return z;
   return div_fast_ok(z, rT) ? div_fast(z, T, rT) : z / T;
 }
-__device__ __forceinline__ float apply_penalty(float z, u32 c, float rep, float pres, float freq) {
-  z = (z > 0.0f) ? (z / rep) : (z * rep);
+// One IEEE step each (rrep = 1 / rep, for the exact fast division).
+__device__ __forceinline__ float apply_penalty(float z, u32 c, float rep, float rrep, float pres, float freq) {
+  z = (z > 0.0f) ? (div_fast_ok(z, rrep) ? div_fast(z, rep, rrep) : z / rep) : (z * rep);
   const float fc = freq * (float)c;
   z = z - fc;
   z = z - pres;

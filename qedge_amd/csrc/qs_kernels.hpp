@@ -124,7 +124,7 @@ struct Args {
 #endif
 
 struct RowP {
-  float T, rT, tp, mp, rep, pres, freq, u;
+  float T, rT, tp, mp, rep, rrep, pres, freq, u;
   int k, kind, hlen;
   bool t_one, topp, pen;
   const int* hist;
@@ -143,6 +143,7 @@ __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   p.topp = p.tp < 1.0f;
   p.mp = a.min_p ? unif(gld(a.min_p + row)) : 0.0f;
   p.rep = a.rep ? unif(gld(a.rep + row)) : 1.0f;
+  p.rrep = 1.0f / p.rep;
   p.pres = a.pres ? unif(gld(a.pres + row)) : 0.0f;
   p.freq = a.freq ? unif(gld(a.freq + row)) : 0.0f;
   p.hlen = a.hist ? (a.hist_len ? (int)uni((u32)gld(a.hist_len + row)) : a.H) : 0;
@@ -297,18 +298,52 @@ __device__ __forceinline__ float elem_z(const Chunk<DT>& ch, const RowP& p, cons
   float z = ch.raw(j, e);
   if (p.pen) {
     const u32 n = pen_count(L, ch, c, j, e);
-    if (n) z = apply_penalty(z, n, p.rep, p.pres, p.freq);
+    if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
+  }
+  return z;
+}
+// The history counts of the thread's elements, two per word as in the table
+// (element j*VL + e in word (j*VL + e) / 2): one vector LDS read per vector.
+template <int DT, typename LT>
+__device__ __forceinline__ void chunk_counts(const LT& L, const Chunk<DT>& ch, int c, u32 (&pw)[kEPT / 2]) {
+  constexpr int VL = Chunk<DT>::VL;
+#pragma unroll
+  for (int j = 0; j < Chunk<DT>::J; ++j) {
+    const int li = ch.base - c * kCH + j * 64 * VL;  // a multiple of VL
+    if (VL == 8) {
+      const uint4 w = *(const uint4*)&pen_table(L)[li >> 1];
+      pw[j * 4 + 0] = w.x;
+      pw[j * 4 + 1] = w.y;
+      pw[j * 4 + 2] = w.z;
+      pw[j * 4 + 3] = w.w;
+    } else {
+      const uint2 w = *(const uint2*)&pen_table(L)[li >> 1];
+      pw[j * 2 + 0] = w.x;
+      pw[j * 2 + 1] = w.y;
+    }
+  }
+}
+// z of element (j, e) with the counts from chunk_counts.
+template <int DT>
+__device__ __forceinline__ float elem_zc(const Chunk<DT>& ch, const RowP& p, const u32 (&pw)[kEPT / 2], int j, int e) {
+  float z = ch.raw(j, e);
+  if (p.pen) {
+    const int i = j * Chunk<DT>::VL + e;
+    const u32 n = (pw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+    if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
   }
   return z;
 }
 // Keys of q = z / T for every element (0 for NaN and invalid elements).
 template <int DT, typename LT>
 __device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, const LT& L, int c, u32 (&kq)[kEPT]) {
+  u32 pw[kEPT / 2];
+  if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
   for (int j = 0; j < Chunk<DT>::J; ++j)
 #pragma unroll
     for (int e = 0; e < Chunk<DT>::VL; ++e) {
-      const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+      const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
       kq[j * Chunk<DT>::VL + e] = skey(q);  // 0 past V (NaN padding)
     }
 }
@@ -599,7 +634,7 @@ __device__ __forceinline__ void chunk_vec(const Args& a, const RowP& p, int row,
     if (p.pen) {
       const int li = i0 + e - c * kCH;
       const u32 n = (L.u.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
-      if (n) z = apply_penalty(z, n, p.rep, p.pres, p.freq);
+      if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
     }
     f(m, e, z, i0 + e);
   }
@@ -1285,11 +1320,13 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
     // z keys
   u32 kz[E];
   u32 m = 0;
+  u32 pw[kEPT / 2];
+  if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
   for (int j = 0; j < J; ++j)
 #pragma unroll
     for (int e = 0; e < VL; ++e) {
-      const u32 kx = skey(elem_z(ch, p, L, c, j, e));  // 0 past V (NaN padding)
+      const u32 kx = skey(elem_zc(ch, p, pw, j, e));  // 0 past V (NaN padding)
       kz[j * VL + e] = kx;
       m = max(m, kx);
     }
@@ -1878,11 +1915,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 
   if (p.kind == kKindGreedy) {
     u64 best = 0;
+    u32 pw[kEPT / 2];
+    if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
     for (int j = 0; j < J; ++j)
 #pragma unroll
       for (int e = 0; e < VL; ++e) {
-        const float z = elem_z(ch, p, L, c, j, e);
+        const float z = elem_zc(ch, p, pw, j, e);
         const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
         best = pk > best ? pk : best;
       }

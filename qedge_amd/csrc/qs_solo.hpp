@@ -133,7 +133,7 @@ __device__ __forceinline__ long long seg_find(const Args& a, const RowP& p, int 
     if (p.pen) {
       const int li = id - c * kCH;
       const u32 n = (L.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
-      if (n) z = apply_penalty(z, n, p.rep, p.pres, p.freq);
+      if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
     }
     v[e] = id < a.V ? val(z, id) : 0ull;
     tot += v[e];
@@ -170,11 +170,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   if (p.kind == kKindGreedy) {
     u64 best = 0;
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+      u32 pw[kEPT / 2];
+      if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
       for (int j = 0; j < J; ++j)
 #pragma unroll
         for (int e = 0; e < VL; ++e) {
-          const float z = elem_z(ch, p, L, c, j, e);
+          const float z = elem_zc(ch, p, pw, j, e);
           const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
           best = pk > best ? pk : best;
         }
@@ -212,11 +214,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     gbest = 0xffffffffu;  // every z NaN: the first id
   } else {
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+      u32 pw[kEPT / 2];
+      if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
       for (int j = 0; j < J; ++j)
 #pragma unroll
         for (int e = 0; e < VL; ++e) {
-          const float z = elem_z(ch, p, L, c, j, e);
+          const float z = elem_zc(ch, p, pw, j, e);
           const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));  // 0 past V (NaN padding)
           kmax = max(kmax, k);
           kmin = k ? min(kmin, k) : kmin;
@@ -247,11 +251,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       const int bl = bitlen(hi - lo);
       const int sh = bl > 8 ? bl - 8 : 0;
       solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+        u32 pw[kEPT / 2];
+        if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
         for (int j = 0; j < J; ++j)
 #pragma unroll
           for (int e = 0; e < VL; ++e) {
-            const u32 k = skey(qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one));
+            const u32 k = skey(qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one));
             if (k >= lo && k <= hi && k) atomicAdd(&L.hc[(hi - k) >> sh], 1u);
           }
       });
@@ -297,12 +303,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   u64 S = 0;
   u32 nz = 0;
   solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+    u32 pw[kEPT / 2];
+    if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       u64 sj = 0;
 #pragma unroll
       for (int e = 0; e < VL; ++e) {
-        const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+        const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
         const u32 k = skey(q);
         const u32 x = wpk(q, k);
         const u64 w = wunpack(x);
@@ -336,11 +344,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         const int bl = bitlen(hi - lo);
         const int sh = bl > 8 ? bl - 8 : 0;
         solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+          u32 pw[kEPT / 2];
+          if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
           for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int e = 0; e < VL; ++e) {
-              const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+              const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
               const u32 k = skey(q);
               if (k && k >= br.lo && k <= br.hi) {
                 const u64 w = wunpack(wpk(q, k));
@@ -433,13 +443,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     lds_sync();
     u32 nzb = 0;  // tokens at or below the bracket with nonzero weight
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+      u32 pw[kEPT / 2];
+      if (p.pen) chunk_counts(L, ch, c, pw);
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         u64 sub = 0;
         u32 ties = 0;
 #pragma unroll
         for (int e = 0; e < VL; ++e) {
-          const float q = qdiv(elem_z(ch, p, L, c, j, e), p.T, p.rT, p.t_one);
+          const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
           const u32 k = skey(q);
           if (!k) continue;
           const int side = bracket_side(br, k);
