@@ -1,20 +1,24 @@
 #!/usr/bin/env python3
 """Decode-step sampler benchmark on one MI355X.
 
-Measures the sampler on the heterogeneous batch workload (B=64 rows of V=248320
-bf16 logits, per-row temperature / top-k / top-p, 10% greedy rows): sampled
-rows/s, µs per step and algorithmic HBM GB/s as a fraction of the 8 TB/s HBM
-roofline.  It also reports µs per step at B=1 (the top-k/top-p/repetition
-workload) and, on rank 0, the torch-CPU restatement of the reference sampler
-timed on the host cores over a bounded sample of the same workload.
+The JSON line's ``value`` is sampled rows/s on the heterogeneous batch (B=64
+rows of V=248320 bf16 logits, per-row temperature / top-k / top-p, 10% greedy
+rows, 10% top-k off), with µs per step and algorithmic HBM GB/s as a fraction
+of the 8 TB/s HBM roofline.  ``workloads`` holds the same figures for every
+synthetic config: the B=1 greedy and T=1 rows of the spiked fp32 config (each
+alone, as a single request runs), the B=1 top-k/top-p/repetition row, the B=64
+batch, the B=256 penalties batch and the B=1024 near-flat top-p batch.  The
+torch-CPU restatement of the reference sampler is timed on the host cores over
+a bounded sample of the B=64 batch, with all threads and with one thread.
 
 A step is one ``qs_sample`` call over one batch.  Inputs are resident in HBM
 before the timed region: the logits are held in several copies that the steps
 rotate through, so that each step reads its batch from HBM rather than from
-the 256 MB last-level cache.  Steps are captured in a HIP graph (the way the
-decode loop runs) and the graph is replayed; the timed region is bracketed by
-``torch.cuda.synchronize()`` and measured with HIP events on the stream the
-kernels run on.
+the 256 MB last-level cache.  Exactly K steps are captured in one HIP graph
+(the way the decode loop runs) and the graph is replayed; the timed region is
+bracketed by ``torch.cuda.synchronize()`` and measured with HIP events on the
+stream the kernels run on.  One step is one kernel launch, so µs per step is
+also the launch's average duration that the roofline fraction uses.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 Prints ONE JSON line.
@@ -46,15 +50,15 @@ def _log(msg: str) -> None:
 class Case:
     """One workload staged on the device with R rotating copies of its inputs."""
 
-    def __init__(self, name: str, device, rotate_bytes: int = ROTATE_BYTES, max_copies: int = 64):
+    def __init__(self, name: str, device, rotate_bytes: int = ROTATE_BYTES, max_copies: int = 64, rows=None):
         import numpy as np
         import torch
 
         from qedge_amd import workloads as W
         from qedge_amd.sampler import Workspace
 
-        self.w = w = W.make(name)
-        self.name = name
+        self.w = w = W.make(name, rows=rows)
+        self.name = name if rows is None else f"{name}[rows {','.join(str(r) for r in rows)}]"
         B, V = w.nrows, w.V
         self.B, self.V = B, V
         if w.dtype == "f32":
@@ -101,37 +105,36 @@ def dispatch_order(w):
     return np.array([r for _, _, r in rank], np.int32)
 
 
-def time_graph(case: Case, steps: int, warmup: int, repeats: int = 5):
-    """µs/step over graph replays of R captured steps; median of `repeats`."""
+def time_graph(case: Case, steps: int, warmup: int, repeats: int = 3):
+    """µs/step over replays of one graph holding exactly ``steps`` steps; median of ``repeats``."""
     import torch
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for i in range(max(warmup, case.R)):
+        for i in range(max(warmup, 1)):
             case.step(i)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(case.R):
+        for i in range(steps):
             case.step(i)
     torch.cuda.synchronize()
-    reps = max(1, math.ceil(steps / case.R))
-    for _ in range(max(1, warmup // case.R)):
-        g.replay()
+    g.replay()  # warm the graph
     torch.cuda.synchronize()
     results = []
+    stream = torch.cuda.current_stream()
     for _ in range(repeats):
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        start.record()
-        for _ in range(reps):
-            g.replay()
-        stop.record()
+        start.record(stream)
+        g.replay()
+        stop.record(stream)
         torch.cuda.synchronize()
-        results.append(start.elapsed_time(stop) * 1000.0 / (reps * case.R))
-    return statistics.median(results), reps * case.R, results
+        results.append(start.elapsed_time(stop) * 1000.0 / steps)
+    del g
+    return statistics.median(results), steps, results
 
 
 def time_eager(case: Case, steps: int):
@@ -146,8 +149,20 @@ def time_eager(case: Case, steps: int):
     return (time.perf_counter() - t0) * 1e6 / steps
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(name: str, budget_s: float = 20.0):
-    """The torch-CPU restatement of the reference sampler on this host's cores."""
+    """The torch-CPU restatement of the reference sampler on this host's cores:
+    median ms/step with torch's default thread count, then with one thread."""
     import numpy as np
     import torch
 
@@ -164,34 +179,41 @@ def cpu_baseline(name: str, budget_s: float = 20.0):
               freq=t(w.freq, torch.float32), history=t(w.history, torch.int32))
     T, P = t(w.temperature, torch.float32), t(w.top_p, torch.float32)
     gen = torch.Generator().manual_seed(0)
-    times = []
-    with torch.inference_mode():
-        for i in range(2):
-            torch_ref.extended_forward(logits, T, P, use_top_p=True, generator=gen, **kw)
-        t_start = time.perf_counter()
-        while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
-            t0 = time.perf_counter()
-            torch_ref.extended_forward(logits, T, P, use_top_p=True, generator=gen, **kw)
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_start > budget_s and len(times) >= 3:
-                break
-        faithful = []
-        for i in range(3):
-            t0 = time.perf_counter()
-            torch_ref.reference_forward(logits, T, P, use_top_p=True, generator=gen)
-            faithful.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+
+    def timed(budget: float, max_steps: int):
+        times = []
+        with torch.inference_mode():
+            torch_ref.extended_forward(logits, T, P, use_top_p=True, generator=gen, **kw)  # warm-up
+            t_start = time.perf_counter()
+            while len(times) < max_steps:
+                t0 = time.perf_counter()
+                torch_ref.extended_forward(logits, T, P, use_top_p=True, generator=gen, **kw)
+                times.append(time.perf_counter() - t0)
+                if time.perf_counter() - t_start > budget and len(times) >= 3:
+                    break
+        return statistics.median(times), len(times)
+
+    threads = torch.get_num_threads()
+    med, n = timed(budget_s * 0.5, 20)
+    torch.set_num_threads(1)
+    try:
+        med1, n1 = timed(budget_s * 0.5, 10)
+    finally:
+        torch.set_num_threads(threads)
     return {
         "value": round(w.nrows / med, 3),
         "unit": "rows/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
         "kind": "port",
-        "sample": (f"{name}: {len(times)} timed steps of B={w.nrows} after 2 warm-up steps, median; "
-                   f"torch-CPU restatement of the reference op sequence with top-k/top-p "
-                   f"(oracle/torch_ref.extended_forward), {torch.get_num_threads()} threads of "
-                   f"{os.cpu_count()} host CPUs"),
+        "sample": (f"{name}: B={w.nrows} rows per step, median of {n} timed steps after one warm-up step; "
+                   f"torch-CPU restatement of the reference op sequence with top-k/top-p and penalties "
+                   f"(oracle/torch_ref.extended_forward) on {threads} threads of {os.cpu_count()} host CPUs "
+                   f"({_cpu_model()}); also {n1} steps on one thread"),
         "ms_per_step": round(med * 1e3, 3),
-        "faithful_ms_per_step": round(statistics.median(faithful) * 1e3, 3),
+        "one_thread": {"value": round(w.nrows / med1, 3), "unit": "rows/s", "cores": 1,
+                       "ms_per_step": round(med1 * 1e3, 3)},
+        "host_cpus": os.cpu_count(),
+        "cpu_model": _cpu_model(),
     }
 
 
@@ -268,19 +290,37 @@ def main() -> int:
     eager_us = time_eager(case, min(args.steps, 500))
     _log(f"eager (host-inclusive): {eager_us:.3f} us/call")
 
+    # every synthetic config (the spiked fp32 one as its two single-request rows)
+    workloads = []
     b1 = None
     if not args.no_b1:
-        c1 = Case(B1_WORKLOAD, dev)
-        b1_us, _, _ = time_graph(c1, args.steps, args.warmup)
-        b1_eager = time_eager(c1, min(args.steps, 500))
-        b1 = {"workload": B1_WORKLOAD, "us_per_step": round(b1_us, 3), "eager_us_per_call": round(b1_eager, 3)}
-        _log(f"B=1 {B1_WORKLOAD}: {b1_us:.3f} us/step graph, {b1_eager:.3f} us/call eager")
+        plan = [("greedy_spikes_f32", [0]), ("greedy_spikes_f32", [1]), (B1_WORKLOAD, None),
+                (WORKLOAD, None), ("penalties_b256_bf16", None), ("flat_topp_b1024_f32", None)]
+        for name, rows in plan:
+            if name == args.workload and rows is None:
+                c, w_us, w_steps = case, us, steps_done
+            else:
+                c = Case(name, dev, rows=rows)
+                w_steps = min(args.steps, 400 if c.B <= 64 else 100)
+                w_us, _, _ = time_graph(c, w_steps, min(args.warmup, 20))
+            gbs = c.alg_bytes / (w_us * 1e-6) / 1e9
+            entry = {"workload": c.name, "B": c.B, "logits": c.w.dtype, "us_per_step": round(w_us, 3),
+                     "rows_per_s": round(c.B / (w_us * 1e-6), 3), "hbm_gbs": round(gbs, 3),
+                     "roofline_frac": round(gbs / HBM_PEAK_GBS, 5), "steps": w_steps}
+            workloads.append(entry)
+            _log(f"{c.name}: {w_us:.3f} us/step, {gbs:.1f} GB/s")
+            if c is not case:
+                del c
+                torch.cuda.empty_cache()
+        b1 = {"workload": B1_WORKLOAD, "us_per_step": next(e["us_per_step"] for e in workloads
+                                                             if e["workload"] == B1_WORKLOAD)}
 
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         cpu = cpu_baseline(args.workload, args.cpu_budget)
-        _log(f"cpu baseline: {cpu['ms_per_step']} ms/step on {cpu['cores']} threads")
+        _log(f"cpu baseline: {cpu['ms_per_step']} ms/step on {cpu['cores']} threads, "
+             f"{cpu['one_thread']['ms_per_step']} ms/step on one")
 
     sec = us * 1e-6
     achieved = case.alg_bytes / sec / 1e9
@@ -300,9 +340,11 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": args.workload, "B": case.B, "V": case.V, "logits": case.w.dtype,
                    "algorithmic_bytes_per_step": case.alg_bytes, "rotating_copies": case.R,
-                   "timing": "HIP-graph replay, HIP events", "eager_us_per_call": round(eager_us, 3)},
+                   "timing": "one HIP graph of exactly `steps` steps, replayed; HIP events",
+                   "eager_us_per_call": round(eager_us, 3)},
         "hbm_gbs": round(achieved, 3),
         "b1": b1,
+        "workloads": workloads,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic_from_profile(args.workload)},
         "cpu_baseline": cpu,
