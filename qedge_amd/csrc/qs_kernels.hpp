@@ -364,7 +364,8 @@ __device__ __forceinline__ u32 arrive(u32* ctr, Scratch& s) {
 __device__ __forceinline__ bool wait_count(const Args& a, int row, const u32* ctr, u32 target, Scratch& s) {
   if (threadIdx.x == 0) {
     bool ok = false;
-    for (u32 it = 0;; ++it) {
+    if (a.spin_limit == 0u) orc(&a.sync[row].status, kStTimeout);  // the test hook: give up at once
+    for (u32 it = 0; a.spin_limit != 0u; ++it) {
       const u32 v = ldc(ctr), st = ldc(&a.sync[row].status);
       if (v >= target) {
         ok = true;
@@ -1132,6 +1133,79 @@ __device__ __forceinline__ void block_sum2(u64& m, u32& c, Scratch& s) {
   m = mt;
 }
 
+// Finish a top-k row whose K (the nk <= 64 held tokens with key >= kk) fits one
+// wave: K is compacted in id order, one wave ranks it in (key desc, id asc)
+// order and moves it there (lane permutes), the top-p rule is applied token by
+// token on the exclusive prefix masses (the same set as by kappa_p and its
+// ties), and the draw is a prefix over K back in id order.  No barrier after
+// the compaction.
+template <typename WPK>
+__device__ __forceinline__ bool finish_small_k(const Args& a, const RowP& p, int row, Lds& L, const Held& h, u32 kk,
+                                               u32 nk, u32 kmax, u64 thr, WPK&& wpk) {
+  nk = uni(nk);
+  u32 cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i)
+    if ((u32)i < h.per && (u32)(h.e[i] >> 32) >= kk) ++cnt;
+  u32 tot;
+  u32 pos = block_excl(cnt, L.s, &tot);
+  u64* kl = L.sel.hm;  // free once the selects are done
+#pragma unroll
+  for (int i = 0; i < kFPer; ++i)
+    if ((u32)i < h.per && (u32)(h.e[i] >> 32) >= kk) kl[pos++] = h.e[i];
+  lds_sync();
+  if (tot != nk) return false;  // K is not what the select counted: cannot happen
+  if (threadIdx.x < 64) {
+    const u32 l = lane_id();
+    const bool have = l < nk;
+    const u64 e = have ? kl[l] : 0ull;
+    const u32 key = (u32)(e >> 32), id = (u32)e;
+    const u32 x = have ? wpk(key) : 0u;
+    const u64 w = wunpack(x);
+    // rank in (key desc, id asc); lanes without a token take the ranks past nk
+    u32 rank = have ? 0u : l;
+    for (u32 j = 0; j < nk; ++j) {
+      const u32 kj = readlane(key, (int)j), ij = readlane(id, (int)j);
+      rank += (have && (kj > key || (kj == key && ij < id))) ? 1u : 0u;
+    }
+    // lane r gets the token of rank r
+    auto push = [&](u32 v) { return (u32)__builtin_amdgcn_ds_permute((int)(rank << 2), (int)v); };
+    const u32 rkey = push(key), rid = push(id), rlo = push((u32)w), rhi = push((u32)(w >> 32));
+    const u64 rw = ((u64)rhi << 32) | rlo;
+    const u64 rin = wave_incl_scan64(rw);
+    const u64 S = readlane64(rin, 63);
+    u64 W = S;
+    u32 klo = kk, idlo = (u32)a.V;
+    bool rkept = l < nk;
+    if (p.topp) {
+      const u64 Tp = mul_frac(S, p.tp);
+      rkept = l < nk && rin - rw <= Tp;  // exclusive prefix within floor(top_p * S)
+      const u64 kb = __ballot(rkept);
+      const int last = 63 - __clzll((long long)kb);  // kept tokens are a prefix of the ranks
+      klo = readlane(rkey, last);
+      idlo = readlane(rid, last);
+      W = readlane64(rin, last);
+    }
+    const u32 kept = popc64(__ballot(rkept && rw != 0ull));
+    // back to id order: lane l reads its token's rank's verdict
+    const bool kp = __builtin_amdgcn_ds_bpermute((int)(rank << 2), rkept ? 1 : 0) != 0 && have;
+    const u64 kw = kp ? w : 0ull;
+    const u64 inc = wave_incl_scan64(kw);
+    const u64 t = mul_frac(W, p.u);
+    const u64 pb = __ballot(kw != 0ull && inc - kw <= t && t < inc);
+    const int src = pb ? __ffsll((long long)pb) - 1 : -1;
+    const long long pick = src >= 0 ? (long long)readlane(id, src) : -1ll;
+    if (l == 0) {
+      L.s.r[11] = pick >= 0 ? 1u : 0u;
+      if (pick >= 0) write_result(a, row, p, pick, W, thr, kPathTopK, 0u, kmax, klo, idlo, kept);
+    }
+  }
+  lds_sync();
+  const bool ok = L.s.r[11] != 0u;
+  lds_sync();
+  return ok;
+}
+
 // Finish a top-k row from its gathered candidates (L.u.fin.ent[0, n), id
 // order): kappa_k (count select), weights and min_p, S, kappa_p (mass select),
 // the draw by an id-order scan.  kmax is the row's largest key of q, klow a
@@ -1156,18 +1230,21 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   for (int i = 0; i < kFPer; ++i) wq[i] = 0u;
   QS_TR(9);
   // kappa_k
-  u32 kk;
+  u32 kk, nk;  // nk: the size of K (tokens with key >= kk)
   if (n < (u32)p.k) {
     if (below_max != 0u) return false;  // tokens left out could belong to K
     kk = 1u;
+    nk = n;
   } else {
     const SelRes q = held_select<false>(a, L, h, wq, max(klow, 1u), kmax, (u64)p.k);
     if (!q.ok) return false;
     kk = q.kappa;
+    nk = q.cnt_above + q.cnt_at;
     // completeness: every token left out has a key of q below kappa_k
     if (below_max != 0u && skey(qdiv(f_of_key(below_max), p.T, p.rT, p.t_one)) >= kk) return false;
   }
   QS_TR(10);
+  if (nk <= 64u) return finish_small_k(a, p, row, L, h, kk, nk, kmax, thr, wpk);
   // weights of K (packed), S and the count of nonzero weights
   u64 S = 0;
   u32 nz = 0;
