@@ -1378,10 +1378,72 @@ __device__ __forceinline__ MassBins mass_bins_split(const MassBins& m, u32 b) {
   n.s2 = 0.0f;
   return n;
 }
+// One wave re-reads segment s and returns, to every lane, the id of the token
+// at which the inclusive id-order total of val(z, key, id) passes t (or -1).
+// The chunk's history table must be built.
+template <int DT, typename LT, typename VF>
+__device__ __forceinline__ long long seg_find(const Args& a, const RowP& p, int row, const LT& L, int s, u64 t,
+                                              VF&& val) {
+  constexpr int VL = Chunk<DT>::VL, J = Chunk<DT>::J;
+  const int c = s / (kWaves * J), w = (s / J) % kWaves, j = s % J;
+  const int l = lane_id();
+  const int i0 = c * kCH + w * kWaveSpan + j * 64 * VL + l * VL;
+  const size_t rowoff = (size_t)row * (size_t)a.row_stride;
+  u32 x[4] = {0u, 0u, 0u, 0u};
+  if (a.vec_ok && i0 + VL <= a.V) {
+    const uint4 v = DT == QS_DTYPE_F32 ? gld((const uint4*)((const float*)a.logits + rowoff + i0))
+                                       : gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+  } else if (DT == QS_DTYPE_F32) {
+    const float* q = (const float*)a.logits + rowoff;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (i0 + e < a.V) x[e] = __float_as_uint(gld(q + i0 + e));
+  } else {
+    const uint16_t* q = (const uint16_t*)a.logits + rowoff;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < a.V) x[e >> 1] |= (u32)gld(q + i0 + e) << ((e & 1) * 16);
+  }
+  u64 v[VL];
+  u64 tot = 0;
+#pragma unroll
+  for (int e = 0; e < VL; ++e) {
+    const int id = i0 + e;
+    float z = DT == QS_DTYPE_F32 ? __uint_as_float(x[e]) : bf16_to_f32((x[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+    if (p.pen) {
+      const int li = id - c * kCH;
+      const u32 n = (pen_table(L)[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
+      if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
+    }
+    v[e] = id < a.V ? val(z, id) : 0ull;
+    tot += v[e];
+  }
+  const u64 inc = wave_incl_scan64(tot);
+  u64 m = inc - tot;
+  long long pick = -1;
+#pragma unroll
+  for (int e = 0; e < VL; ++e) {
+    if (m <= t && t < m + v[e]) pick = i0 + e;
+    m += v[e];
+  }
+  const u64 bal = __ballot(pick >= 0);
+  if (!bal) return -1;
+  const int src = __ffsll((long long)bal) - 1;
+  return (long long)readlane((u32)pick, src);
+}
+
 // Per-row data of top-k-off rows: the row's bin masses [kRounds][kNB] u64
-// (summed by atomics), then the listed tokens [G][kLC].
+// (summed by atomics), the listed tokens [G][kLC], then the kept mass of every
+// segment known before the final selection [G][kSegMax] (a segment is one
+// wave's vector span of a chunk, 64 * VL ids: kWaves * J of them per chunk).
+constexpr int kSegMax = 32;
 __device__ __forceinline__ u64* row_hist(const Args& a, int row) { return row_data(a, row); }
 __device__ __forceinline__ u64* list_base(const Args& a, int row) { return row_data(a, row) + (size_t)kRounds * kNB; }
+__device__ __forceinline__ u64* seg_base(const Args& a, int row) { return list_base(a, row) + (size_t)a.G * kLC; }
 
 // ---------------------------------------------------------------- the streaming kernel
 
@@ -1640,6 +1702,17 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       }
     }
     QS_TR(5);
+    if (!p.topp) {  // every weight is kept: the segments' masses
+      u64* sg = seg_base(a, row) + (size_t)c * kSegMax;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        u64 sj = 0;
+#pragma unroll
+        for (int e = 0; e < VL; ++e) sj += wunpack(wp[j * VL + e]);
+        sj = wave_sum64(sj);
+        if (lane_id() == 0) stc(&sg[wave_id() * J + j], sj);
+      }
+    }
     block_sum2(Sc, nz, L.s);  // its barriers also complete the histogram
     if (threadIdx.x == 0) {
       stc(&sl[c].b, Sc);
@@ -1720,15 +1793,23 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
         QS_TR(10 + 4 * r);
       }
       if (ok) {
-        // mass above the bracket, and the bracket's tokens listed in id order
+        // mass above the bracket (per segment too), and the bracket's tokens listed in id order
         u64 above = 0;
         u32 cnt[J];
+        u64* sg = seg_base(a, row) + (size_t)c * kSegMax;
 #pragma unroll
-        for (int j = 0; j < J; ++j) cnt[j] = 0;
+        for (int j = 0; j < J; ++j) {
+          cnt[j] = 0;
+          u64 sj = 0;
 #pragma unroll
-        for (int i = 0; i < E; ++i) {
-          above += ((abv >> i) & 1u) ? wunpack(wp[i]) : 0ull;
-          cnt[i / VL] += (inb >> i) & 1u;
+          for (int e = 0; e < VL; ++e) {
+            const int i = j * VL + e;
+            sj += ((abv >> i) & 1u) ? wunpack(wp[i]) : 0ull;
+            cnt[j] += (inb >> i) & 1u;
+          }
+          above += sj;
+          sj = wave_sum64(sj);
+          if (lane_id() == 0) stc(&sg[wave_id() * J + j], sj);
         }
         u32 na = (u32)__popc(abv);
         block_sum2(above, na, L.s);
@@ -1792,6 +1873,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   if (st != 0u || kstar == 0u) return st ? st : kStIncomplete;
   // per-chunk kept masses and tie counts in L.cmass / L.cties
   u64 W = 0, wt = 0;
+  u32 nlist = 0;  // listed tokens (in L.u.fin.ent, id order)
   u32 klo = 1u, jties = 0xffffffffu, kept = 0, idlo = (u32)a.V;
   bool fine = true;
   auto wpk = [&](u32 key) -> u32 {
@@ -1811,7 +1893,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     const u64 Ahi = A;
     u32 nat = 0;
     u32 mx[3];
-    const u32 n = gather_lds(a, list_base(a, row), kLC, [&](int cc, u32(&)[3]) -> u32 {
+    const u32 n = nlist = gather_lds(a, list_base(a, row), kLC, [&](int cc, u32(&)[3]) -> u32 {
       const u64 cv = ldc(&sl[cc].c);
       L.cmass[cc] = ldc(&sl[cc].b);
       nat = (u32)cv;
@@ -1939,22 +2021,58 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   lds_sync();
   if (owner < 0) return kStIncomplete;
   QS_TR(23);
-  // re-read the owner chunk and locate the token
-  load_chunk<DT>(a, row, owner, ch);
+  // the segment of the owner chunk holding the draw: the segments' masses known
+  // before the selection, plus (top-p) the listed tokens kept
+  (void)jl;
+  const int nsg = kWaves * J;
+  const u64* sg = seg_base(a, row) + (size_t)owner * kSegMax;
+  if ((int)threadIdx.x < nsg) L.cmass[threadIdx.x] = ldc(&sg[threadIdx.x]);
+  lds_sync();
+  if (p.topp) {
+    for (u32 i = threadIdx.x; i < nlist; i += kThreads) {
+      const u64 e = L.u.fin.ent[i];
+      const u32 key = (u32)(e >> 32), id = (u32)e;
+      if ((int)(id / (u32)kCH) == owner && (key > klo || (key == klo && id <= idlo))) {
+        const u64 w = wf(key);
+        if (w) atomicAdd(&L.cmass[(id - (u32)owner * kCH) / (64 * VL)], w);
+      }
+    }
+    lds_sync();
+  }
+  if (threadIdx.x < 64) {
+    const int l = (int)lane_id();
+    const u64 m = l < nsg ? L.cmass[l] : 0ull;
+    const u64 inc = wave_incl_scan64(m);
+    const u64 bal = __ballot(m && inc - m <= tin && tin < inc);
+    if (l == 0) L.s.r[15] = bal ? (u32)(__ffsll((long long)bal) - 1) : 0xffffffffu;
+    const int src = bal ? __ffsll((long long)bal) - 1 : 0;
+    const u64 ex = readlane64(inc - m, src);
+    if (l == 0) L.s.r64[13] = tin - ex;
+  }
+  lds_sync();
+  const u32 sloc = L.s.r[15];
+  const u64 tin2 = L.s.r64[13];
+  lds_sync();
+  if (sloc == 0xffffffffu) return kStIncomplete;
   if (p.pen) pen_build(p, owner, L);
-  u32 kq[E];
-  chunk_qkeys<DT>(ch, p, L, owner, kq);
-  if (p.pen) lds_sync();
-  const bool ties_on = jties != 0xffffffffu;
-  auto kw = [&](int i) -> KW {
-    u64 w = weight_of(f_of_key(kq[i]), kq[i], qs, kstar, SH);
-    w = w >= thr ? w : 0ull;
-    const bool above = ties_on ? kq[i] > klo : true;
-    return KW{above ? w : 0ull, ties_on && w && kq[i] == klo};
-  };
   QS_TR(24);
-  const int pick = chunk_locate<DT>(ch, kw, wt, jl, tin, L);
-  if (pick < 0) return kStIncomplete;
+  if (threadIdx.x < 64) {
+    const bool topp = p.topp;
+    const long long id = seg_find<DT>(a, p, row, L, owner * nsg + (int)sloc, tin2, [&](float z, int i) -> u64 {
+      const float q = qdiv(z, p.T, p.rT, p.t_one);
+      const u32 k = skey(q);
+      u64 w = weight_of(q, k, qs, kstar, SH);
+      w = w >= thr ? w : 0ull;
+      if (!topp) return w;
+      return (k > klo || (k == klo && (u32)i <= idlo)) ? w : 0ull;
+    });
+    if (threadIdx.x == 0) L.s.r[15] = id < 0 ? 0xffffffffu : (u32)id;
+  }
+  lds_sync();
+  const u32 pk = L.s.r[15];
+  lds_sync();
+  if (pk == 0xffffffffu) return kStIncomplete;
+  const long long pick = (long long)pk;
   write_result(a, row, p, pick, W, thr, p.topp ? kPathMassTopP : kPathMassAll, 0u, kstar, p.topp ? klo : 1u,
                p.topp ? idlo : (u32)a.V, kept);
   QS_TR(25);

@@ -94,64 +94,6 @@ __device__ __forceinline__ int bracket_side(const Bracket& br, u32 k) {
   return k > br.hi ? 0 : (k < br.lo ? 2 : 1);
 }
 
-// One wave re-reads segment s and returns, to every lane, the id of the token
-// at which the inclusive id-order total of val(z, key, id) passes t (or -1).
-// The chunk's history table must be built.
-template <int DT, typename VF>
-__device__ __forceinline__ long long seg_find(const Args& a, const RowP& p, int row, const SoloLds& L, int s, u64 t,
-                                              VF&& val) {
-  constexpr int VL = Chunk<DT>::VL, J = Chunk<DT>::J;
-  const int c = s / (kWaves * J), w = (s / J) % kWaves, j = s % J;
-  const int l = lane_id();
-  const int i0 = c * kCH + w * kWaveSpan + j * 64 * VL + l * VL;
-  const size_t rowoff = (size_t)row * (size_t)a.row_stride;
-  u32 x[4] = {0u, 0u, 0u, 0u};
-  if (a.vec_ok && i0 + VL <= a.V) {
-    const uint4 v = DT == QS_DTYPE_F32 ? gld((const uint4*)((const float*)a.logits + rowoff + i0))
-                                       : gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
-    x[0] = v.x;
-    x[1] = v.y;
-    x[2] = v.z;
-    x[3] = v.w;
-  } else if (DT == QS_DTYPE_F32) {
-    const float* q = (const float*)a.logits + rowoff;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (i0 + e < a.V) x[e] = __float_as_uint(gld(q + i0 + e));
-  } else {
-    const uint16_t* q = (const uint16_t*)a.logits + rowoff;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (i0 + e < a.V) x[e >> 1] |= (u32)gld(q + i0 + e) << ((e & 1) * 16);
-  }
-  u64 v[VL];
-  u64 tot = 0;
-#pragma unroll
-  for (int e = 0; e < VL; ++e) {
-    const int id = i0 + e;
-    float z = DT == QS_DTYPE_F32 ? __uint_as_float(x[e]) : bf16_to_f32((x[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-    if (p.pen) {
-      const int li = id - c * kCH;
-      const u32 n = (L.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
-      if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
-    }
-    v[e] = id < a.V ? val(z, id) : 0ull;
-    tot += v[e];
-  }
-  const u64 inc = wave_incl_scan64(tot);
-  u64 m = inc - tot;
-  long long pick = -1;
-#pragma unroll
-  for (int e = 0; e < VL; ++e) {
-    if (m <= t && t < m + v[e]) pick = i0 + e;
-    m += v[e];
-  }
-  const u64 bal = __ballot(pick >= 0);
-  if (!bal) return -1;
-  const int src = __ffsll((long long)bal) - 1;
-  return (long long)readlane((u32)pick, src);
-}
-
 template <int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_solo(Args a) {
   __shared__ SoloLds L;

@@ -52,7 +52,7 @@ bool layout_for(int B, int V, Layout* L) {
   if (L->R > kRegionCap) L->R = kRegionCap;
   L->SH = shift_of(V);
   const long long cand = (long long)L->G * L->R;
-  const long long mass = (long long)kRounds * kNB + (long long)L->G * kLC;
+  const long long mass = (long long)kRounds * kNB + (long long)L->G * (kLC + kSegMax);
   L->dpr = cand > mass ? cand : mass;
   // one row's block: counters, result, slots, data
   L->off_sync = 0;
