@@ -953,34 +953,46 @@ struct SelRes {
   u32 kappa, cnt_above, cnt_at;
   u64 mass_above, mass_at;
   bool ok;
+  u32 total_cnt;   // the first round's totals over the range
+  u64 total_mass;
 };
+// With frac >= 0 (by mass) the target is floor(frac * total), the total being
+// the range's mass, found in the first round; the totals are returned.  The
+// histogram has two buffers: a round clears the next one's.
 template <bool BY_MASS, typename LT>
 __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& h, const u32 (&wq)[kFPer], u32 lo,
-                                              u32 hi, u64 target) {
+                                              u32 hi, u64 target, float frac = -1.0f) {
   (void)a;
   SelRes r;
   r.kappa = r.cnt_above = r.cnt_at = 0u;
   r.mass_above = r.mass_at = 0ull;
   r.ok = false;
+  r.total_cnt = 0u;
+  r.total_mass = 0ull;
+  for (int b = threadIdx.x; b < kNB; b += kThreads) {
+    L.sel.hc[b] = 0u;
+    L.sel.hm[b] = 0ull;
+  }
+  lds_sync();
   for (int round = 0; round < 6; ++round) {
     const int bl = bitlen(hi - lo);
     const int sh = bl > 8 ? bl - 8 : 0;
+    const int cur = (round & 1) * kNB, nxt = kNB - cur;
     if (round < 4) QS_TRA(15 + 3 * round);
-    for (int b = threadIdx.x; b < 256; b += kThreads) {
-      L.sel.hc[b] = 0u;
-      L.sel.hm[b] = 0ull;
-    }
-    lds_sync();
 #pragma unroll
     for (int i = 0; i < kFPer; ++i) {
       if ((u32)i < h.per) {
         const u32 key = (u32)(h.e[i] >> 32);
         if (key >= lo && key <= hi && (!BY_MASS || wq[i] != 0u)) {
           const u32 b = (hi - key) >> sh;
-          atomicAdd(&L.sel.hc[b], 1u);
-          if (BY_MASS) atomicAdd(&L.sel.hm[b], wunpack(wq[i]));
+          atomicAdd(&L.sel.hc[cur + b], 1u);
+          if (BY_MASS) atomicAdd(&L.sel.hm[cur + b], wunpack(wq[i]));
         }
       }
+    }
+    for (int b = threadIdx.x; b < kNB; b += kThreads) {
+      L.sel.hc[nxt + b] = 0u;
+      L.sel.hm[nxt + b] = 0ull;
     }
     lds_sync();
     if (round < 4) QS_TRA(16 + 3 * round);
@@ -990,8 +1002,8 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
       u64 m4[4], ms = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        c4[j] = L.sel.hc[4 * l + j];
-        m4[j] = BY_MASS ? L.sel.hm[4 * l + j] : 0ull;
+        c4[j] = L.sel.hc[cur + 4 * l + j];
+        m4[j] = BY_MASS ? L.sel.hm[cur + 4 * l + j] : 0ull;
         cs += c4[j];
         ms += m4[j];
       }
@@ -999,7 +1011,19 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
       const u64 mi = BY_MASS ? wave_incl_scan64(ms) : 0ull;
       u32 cb = ci - cs;
       u64 mb = mi - ms;
-      if (l == 0) L.s.r[4] = 0xffffffffu;
+      if (round == 0 && frac >= 0.0f) {
+        const u64 tm = readlane64(mi, 63);
+        target = mul_frac(tm, frac);
+        if (l == 0) {
+          L.s.r64[10] = tm;
+          L.s.r[13] = readlane(ci, 63);
+        }
+      }
+      if (l == 0) {
+        L.s.r[4] = 0xffffffffu;
+        L.s.r[7] = 0u;  // for a direct resolution
+        L.s.r[8] = 0xffffffffu;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool hit = BY_MASS ? (mb <= target && target < mb + m4[j]) : (cb < target && target <= cb + c4[j]);
@@ -1016,6 +1040,11 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
     }
     lds_sync();
     if (round < 4) QS_TRA(17 + 3 * round);
+    if (round == 0 && frac >= 0.0f) {
+      r.total_mass = uni64(L.s.r64[10]);
+      r.total_cnt = uni(L.s.r[13]);
+      target = mul_frac(r.total_mass, frac);
+    }
     const u32 b = uni(L.s.r[4]);
     const u32 cb = uni(L.s.r[5]), cnt_b = uni(L.s.r[6]);
     const u64 mb = uni64(L.s.r64[4]), mass_b = uni64(L.s.r64[5]);
@@ -1041,11 +1070,6 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
     lo = nlo;
     if (cnt_b <= (u32)kDirect) {
       // the bin's entries, ranked directly: entry x by the 8 threads 8x..8x+7
-      if (threadIdx.x == 0) {
-        L.s.r[7] = 0u;
-        L.s.r[8] = 0xffffffffu;
-      }
-      lds_sync();
 #pragma unroll
       for (int i = 0; i < kFPer; ++i) {
         if ((u32)i < h.per) {
@@ -1245,7 +1269,8 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   }
   QS_TR(10);
   if (nk <= 64u) return finish_small_k(a, p, row, L, h, kk, nk, kmax, thr, wpk);
-  // weights of K (packed), S and the count of nonzero weights
+  // weights of K (packed); S and the count of nonzero weights (with top-p, as the
+  // totals of the boundary's select)
   u64 S = 0;
   u32 nz = 0;
 #pragma unroll
@@ -1257,13 +1282,14 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
       nz += wq[i] ? 1u : 0u;
     }
   }
-  block_sum2(S, nz, L.s);
+  if (!p.topp) block_sum2(S, nz, L.s);
   u32 klo = kk, jties = 0xffffffffu, kept = nz;
   u64 W = S, wt = 0;
   QS_TR(11);
   if (p.topp) {
+    const SelRes q = held_select<true>(a, L, h, wq, kk, kmax, 0ull, p.tp);
+    S = q.total_mass;
     const u64 Tp = mul_frac(S, p.tp);
-    const SelRes q = held_select<true>(a, L, h, wq, kk, kmax, Tp);
     if (!q.ok) return false;
     klo = q.kappa;
     wt = wf(klo);  // every token at kappa_p has this weight

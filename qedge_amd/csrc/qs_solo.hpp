@@ -29,8 +29,8 @@ struct SoloFin {
   u64 lw[kDirect];
 };
 struct SoloSel {
-  u32 hc[kNB];
-  u64 hm[kNB];
+  u32 hc[2 * kNB];  // two buffers
+  u64 hm[2 * kNB];
 };
 struct SoloLds {
   union {
