@@ -1230,6 +1230,155 @@ __device__ __forceinline__ bool finish_small_k(const Args& a, const RowP& p, int
   return ok;
 }
 
+// ---------------------------------------------------------------- wave sorting networks
+
+// The value of lane l ^ J, by DPP moves within rows of 16 lanes and the
+// permlane swaps across them (no LDS traffic).
+template <int J>
+__device__ __forceinline__ u32 xlane(u32 v) {
+  const u32 l = lane_id();
+  if constexpr (J == 1) {
+    return (u32)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xf, 0xf, true);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (J == 2) {
+    return (u32)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xf, 0xf, true);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (J == 4) {
+    const u32 up = (u32)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xf, 0xf, true);  // row_shl 4: lane l + 4
+    const u32 dn = (u32)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xf, 0xf, true);  // row_shr 4: lane l - 4
+    return (l & 4u) ? dn : up;
+  } else if constexpr (J == 8) {
+    return (u32)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xf, 0xf, true);  // row_ror 8
+  } else if constexpr (J == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // rows (0,0,2,2) and (1,1,3,3)
+    return (l & 16u) ? (u32)s[0] : (u32)s[1];
+  } else {
+    static_assert(J == 32, "lane distances 1 .. 32");
+    const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // halves (lo, lo) and (hi, hi)
+    return (l & 32u) ? (u32)s[0] : (u32)s[1];
+  }
+}
+// Compare-exchange with lane l ^ J: the lane keeps the larger of the pair iff
+// (it is the lower lane) == desc.
+template <int J>
+__device__ __forceinline__ u64 cmpx(u64 v, bool desc) {
+  const u64 o = ((u64)xlane<J>((u32)(v >> 32)) << 32) | xlane<J>((u32)v);
+  const bool big = ((lane_id() & (u32)J) == 0u) == desc;
+  return big ? (o > v ? o : v) : (o < v ? o : v);
+}
+// One value per lane, sorted over the wave (bitonic network): descending or ascending.
+template <bool DESC>
+__device__ __forceinline__ u64 wave_sort(u64 v) {
+  const u32 l = lane_id();
+  auto d = [&](u32 k) { return ((l & k) == 0u) == DESC; };  // the block of size k runs descending
+  v = cmpx<1>(v, d(2));
+  v = cmpx<2>(v, d(4));
+  v = cmpx<1>(v, d(4));
+  v = cmpx<4>(v, d(8));
+  v = cmpx<2>(v, d(8));
+  v = cmpx<1>(v, d(8));
+  v = cmpx<8>(v, d(16));
+  v = cmpx<4>(v, d(16));
+  v = cmpx<2>(v, d(16));
+  v = cmpx<1>(v, d(16));
+  v = cmpx<16>(v, d(32));
+  v = cmpx<8>(v, d(32));
+  v = cmpx<4>(v, d(32));
+  v = cmpx<2>(v, d(32));
+  v = cmpx<1>(v, d(32));
+  v = cmpx<32>(v, DESC);
+  v = cmpx<16>(v, DESC);
+  v = cmpx<8>(v, DESC);
+  v = cmpx<4>(v, DESC);
+  v = cmpx<2>(v, DESC);
+  v = cmpx<1>(v, DESC);
+  return v;
+}
+// A bitonic sequence over the wave, sorted descending.
+__device__ __forceinline__ u64 wave_merge_desc(u64 v) {
+  v = cmpx<32>(v, true);
+  v = cmpx<16>(v, true);
+  v = cmpx<8>(v, true);
+  v = cmpx<4>(v, true);
+  v = cmpx<2>(v, true);
+  v = cmpx<1>(v, true);
+  return v;
+}
+
+// Finish a top-k row with k < 64 from at most kThreads gathered candidates
+// (L.u.fin.ent[0, n), id order): every wave sorts 64 of them by (key desc, id
+// asc), a tree of wave merges (each keeps the 64 largest of two sorted lists)
+// leaves the row's 64 largest in wave 0, which applies top-k (ties kept), min_p
+// and top-p to them and draws in id order.  The same sets and draw as
+// finish_small_k.  Returns 1 when done, 0 when the row must go to the exact
+// path, -1 when ties at kappa_k may reach past the 64 kept (the general
+// finisher takes the row).
+template <typename WPK>
+__device__ __forceinline__ int finish_sorted(const Args& a, const RowP& p, int row, Lds& L, u32 n, u32 kmax,
+                                             u32 below_max, u64 thr, WPK&& wpk) {
+  const u32 t = threadIdx.x, w = wave_id(), l = lane_id();
+  const u64 e = t < n ? L.u.fin.ent[t] : 0ull;
+  u64 v = e ? (e & 0xffffffff00000000ull) | (u64)(~(u32)e) : 0ull;  // (key, ~id); 0 for no token
+  v = wave_sort<true>(v);
+  const u32 nw = uni((n + 63u) / 64u);  // waves holding candidates
+  for (u32 step = 1, lev = 0; step < nw; step <<= 1, ++lev) {
+    u64* buf = L.sel.hm + (lev & 1u) * kThreads;  // two buffers: one barrier per level
+    buf[t] = v;
+    lds_sync();
+    if ((w & (2u * step - 1u)) == 0u && w + step < nw) {
+      const u64 b = buf[(w + step) * 64u + 63u - l];  // the partner's list, reversed
+      v = wave_merge_desc(b > v ? b : v);
+    }
+  }
+  if (w == 0u) {
+    const u32 key = (u32)(v >> 32), id = ~(u32)v;
+    const bool have = v != 0ull;
+    int res = 1;
+    u32 kk = 1u;  // fewer candidates than k: every one of them (if none was left out)
+    if (n < (u32)p.k) {
+      if (below_max != 0u) res = 0;
+    } else {
+      kk = readlane(key, p.k - 1);
+      // completeness: every token left out has a key of q below kappa_k
+      if (below_max != 0u && skey(qdiv(f_of_key(below_max), p.T, p.rT, p.t_one)) >= kk) res = 0;
+      if (n > 64u && readlane(key, 63) == kk) res = -1;  // ties at kappa_k may go on past the 64
+    }
+    if (res == 1) {
+      const bool inK = have && key >= kk;
+      const u64 wv = inK ? wunpack(wpk(key)) : 0ull;
+      const u64 rin = wave_incl_scan64(wv);
+      const u64 S = readlane64(rin, 63);
+      u64 W = S;
+      u32 klo = kk, idlo = (u32)a.V;
+      bool kept = inK;
+      if (p.topp) {
+        const u64 Tp = mul_frac(S, p.tp);
+        kept = inK && rin - wv <= Tp;  // exclusive prefix within floor(top_p * S): a prefix of the order
+        const u64 kb = __ballot(kept);
+        const int last = 63 - __clzll((long long)kb);
+        klo = readlane(key, last);
+        idlo = readlane(id, last);
+        W = readlane64(rin, last);
+      }
+      const u32 nkept = popc64(__ballot(kept && wv != 0ull));
+      // the draw: the kept tokens in id order (lane of origin as payload)
+      const u64 sv = wave_sort<false>(kept ? ((u64)id << 32) | l : ~0ull);
+      const int src = (int)(u32)sv;
+      const u32 wlo = (u32)__shfl((int)(u32)wv, src & 63), whi = (u32)__shfl((int)(u32)(wv >> 32), src & 63);
+      const u64 wk = sv != ~0ull ? ((u64)whi << 32) | wlo : 0ull;
+      const u64 inc = wave_incl_scan64(wk);
+      const u64 tt = mul_frac(W, p.u);
+      const u64 pb = __ballot(wk != 0ull && inc - wk <= tt && tt < inc);
+      const long long pick = pb ? (long long)readlane((u32)(sv >> 32), __ffsll((long long)pb) - 1) : -1ll;
+      if (pick < 0) res = 0;
+      if (l == 0u && pick >= 0) write_result(a, row, p, pick, W, thr, kPathTopK, 0u, kmax, klo, idlo, nkept);
+    }
+    if (l == 0u) L.s.r[11] = (u32)res;
+  }
+  lds_sync();
+  const int res = (int)L.s.r[11];
+  lds_sync();
+  return res;
+}
+
 // Finish a top-k row from its gathered candidates (L.u.fin.ent[0, n), id
 // order): kappa_k (count select), weights and min_p, S, kappa_p (mass select),
 // the draw by an id-order scan.  kmax is the row's largest key of q, klow a
@@ -1247,6 +1396,10 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
     return wunpack(x) >= thr ? x : 0u;
   };
   auto wf = [&](u32 key) -> u64 { return wunpack(wpk(key)); };
+  if (n <= (u32)kThreads && (u32)p.k < 64u) {
+    const int r = finish_sorted(a, p, row, L, n, kmax, below_max, thr, wpk);
+    if (r >= 0) return r != 0;
+  }
   Held h;
   hold_entries(L, n, h);
   u32 wq[kFPer];
