@@ -607,40 +607,24 @@ __device__ __forceinline__ int chunk_locate(const Chunk<DT>& ch, F&& kw, u64 wt,
 // the last kept tie.  Serves every row the fast paths leave (top-k above
 // kTopkMax, overflows, time-outs, rows without weights).
 
-// Calls f(m, e, z, id) for the valid elements of vector m of chunk c: thread t
-// holds vector t + m * kThreads of the chunk (VL logits).
+// Calls f(z, id) for element s of chunk c of this thread, id = c * kCH + s *
+// kThreads + t (when below V): one logit per thread and step, so that the
+// steps of a chunk run in id order and the exact path stays small.
+constexpr int kElemSteps = kCH / kThreads;
 template <int DT, typename F>
-__device__ __forceinline__ void chunk_vec(const Args& a, const RowP& p, int row, int c, int m, const Lds& L, F&& f) {
-  constexpr int VL = DT == QS_DTYPE_F32 ? 4 : 8;
-  const int i0 = c * kCH + (m * kThreads + (int)threadIdx.x) * VL;
+__device__ __forceinline__ void chunk_elem(const Args& a, const RowP& p, int row, int c, int s, const Lds& L, F&& f) {
+  const int id = c * kCH + s * kThreads + (int)threadIdx.x;
+  if (id >= a.V) return;
   const size_t rowoff = (size_t)row * (size_t)a.row_stride;
-  u32 x[4] = {0u, 0u, 0u, 0u};
-  if (a.vec_ok && i0 + VL <= a.V) {
-    const uint4 v = DT == QS_DTYPE_F32 ? gld((const uint4*)((const float*)a.logits + rowoff + i0))
-                                       : gld((const uint4*)((const uint16_t*)a.logits + rowoff + i0));
-    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
-  } else if (DT == QS_DTYPE_F32) {
-    const float* q = (const float*)a.logits + rowoff;
-    for (int e = 0; e < 4; ++e)
-      if (i0 + e < a.V) x[e] = __float_as_uint(gld(q + i0 + e));
-  } else {
-    const uint16_t* q = (const uint16_t*)a.logits + rowoff;
-    for (int e = 0; e < 8; ++e)
-      if (i0 + e < a.V) x[e >> 1] |= (u32)gld(q + i0 + e) << ((e & 1) * 16);
+  float z = DT == QS_DTYPE_F32 ? gld((const float*)a.logits + rowoff + id)
+                               : bf16_to_f32((u32)gld((const uint16_t*)a.logits + rowoff + id));
+  if (p.pen) {
+    const int li = id - c * kCH;
+    const u32 n = (L.u.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
+    if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
   }
-#pragma unroll
-  for (int e = 0; e < VL; ++e) {
-    if (i0 + e >= a.V) break;
-    float z = DT == QS_DTYPE_F32 ? __uint_as_float(x[e]) : bf16_to_f32((x[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-    if (p.pen) {
-      const int li = i0 + e - c * kCH;
-      const u32 n = (L.u.pen[li >> 1] >> ((li & 1) * 16)) & 0xffffu;
-      if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
-    }
-    f(m, e, z, i0 + e);
-  }
+  f(z, id);
 }
-constexpr int vecs_per_chunk(int DT) { return kCH / (DT == QS_DTYPE_F32 ? 4 : 8) / kThreads; }
 
 // f(z, id) over the whole row (chunk by chunk, penalty table per chunk).
 template <int DT, typename F>
@@ -649,10 +633,18 @@ __device__ __forceinline__ void row_pass(const Args& a, const RowP& p, int row, 
   for (int c = 0; c < a.G; ++c) {
     if (p.pen) pen_build(p, c, L);
 #pragma unroll 1
-    for (int m = 0; m < vecs_per_chunk(DT); ++m)
-      chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int id) { f(z, id); });
+    for (int s = 0; s < kElemSteps; ++s) chunk_elem<DT>(a, p, row, c, s, L, f);
     if (p.pen) lds_sync();
   }
+}
+
+// The launch's Args read afresh from the kernel-argument segment (the kernel's
+// only explicit argument, at offset 0).  Code that is rarely taken reads its
+// arguments through this, so that their loads are not merged with those of the
+// streaming paths and the merged values do not stay in scalar registers across
+// the whole kernel.
+__device__ __forceinline__ const Args& kernel_args() {
+  return *(const Args*)__builtin_amdgcn_kernarg_segment_ptr();
 }
 
 template <int DT>
@@ -753,8 +745,8 @@ __device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, 
     u64 cm = 0;
     u32 ct = 0;
 #pragma unroll 1
-    for (int m = 0; m < vecs_per_chunk(DT); ++m)
-      chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int) {
+    for (int m = 0; m < kElemSteps; ++m)
+      chunk_elem<DT>(a, p, row, c, m, L, [&](float z, int) {
         u32 k;
         const u64 w = key_w(z, k);
         if (k >= kk && (ties_on ? k > klo : k >= klo)) cm += w;
@@ -767,14 +759,14 @@ __device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, 
     const bool has_pick = pick < 0 && t < acc + kc;
     const bool has_tie = ties_on && idlo < 0 && jties > ties_before && jties <= ties_before + ct;
     if (has_pick || has_tie) {
-      // id-order walk of the chunk: vector m of every thread, then m + 1
+      // id-order walk of the chunk: step m of every thread, then m + 1
       u64 run_m = acc_above;
       u32 run_t = ties_before;
-  #pragma unroll 1
-    for (int m = 0; m < vecs_per_chunk(DT); ++m) {
+#pragma unroll 1
+      for (int m = 0; m < kElemSteps; ++m) {
         u64 vm = 0;
         u32 vt = 0;
-        chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int) {
+        chunk_elem<DT>(a, p, row, c, m, L, [&](float z, int) {
           u32 k;
           const u64 w = key_w(z, k);
           if (k >= kk && (ties_on ? k > klo : k >= klo)) vm += w;
@@ -792,7 +784,7 @@ __device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, 
         lds_sync();
         u64 mb = run_m + mex;
         u32 tb = run_t + tex;
-        chunk_vec<DT>(a, p, row, c, m, L, [&](int, int, float z, int id) {
+        chunk_elem<DT>(a, p, row, c, m, L, [&](float z, int id) {
           u32 k;
           const u64 w = key_w(z, k);
           const bool above = k >= kk && (ties_on ? k > klo : k >= klo);
@@ -2081,6 +2073,60 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     QS_TR(21);
     if (n == 0xffffffffu || n == 0u) {
       fine = false;
+    } else if (n <= 64u) {
+      // A short list: one wave orders it by (key desc, id asc), keeps the prefix
+      // whose exclusive mass stays within Tp - A, and adds the kept weights to
+      // their chunks (no tie accounting: each kept token is known).
+      nat = block_sum(nat, L.s);
+      if (threadIdx.x < 64) {
+        const u32 l = lane_id();
+        const bool have = l < n;
+        const u64 e = have ? L.u.fin.ent[l] : 0ull;
+        const u32 key = (u32)(e >> 32), id = (u32)e;
+        const u64 wv = have ? wf(key) : 0ull;
+        u64 pre = 0;  // mass of the tokens before this one in (key desc, id asc) order
+        for (u32 j = 0; j < n; ++j) {
+          const u32 kj = readlane(key, (int)j), ij = readlane(id, (int)j);
+          const u64 wj = readlane64(wv, (int)j);
+          pre += (kj > key || (kj == key && ij < id)) ? wj : 0ull;
+        }
+        const u64 T1 = Tp - Ahi;
+        const bool kp = have && wv != 0ull && pre <= T1;
+        // the last kept token: the largest prefix among the kept
+        const u64 lastpre = kp ? pre : 0ull;
+        u64 mp = lastpre;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const u64 x = ((u64)(u32)__shfl_xor((int)(u32)(mp >> 32), o) << 32) | (u32)__shfl_xor((int)(u32)mp, o);
+          mp = x > mp ? x : mp;
+        }
+        const u64 lb = __ballot(kp && pre == mp);
+        const u32 nkp = popc64(__ballot(kp));
+        const u64 inc = pre + wv;
+        if (kp) atomicAdd(&L.cmass[id / (u32)kCH], wv);
+        const int src = lb ? __ffsll((long long)lb) - 1 : 0;
+        const u32 klast = readlane(key, src), ilast = readlane(id, src);
+        const u64 wlast = readlane64(inc, src);
+        if (l == 0u) {
+          L.s.r[13] = lb ? nkp : 0u;
+          L.s.r[14] = klast;
+          L.s.r[15] = ilast;
+          L.s.r64[14] = Ahi + wlast;
+        }
+      }
+      for (int cc = threadIdx.x; cc < a.G; cc += kThreads) L.cties[cc] = 0u;
+      lds_sync();
+      const u32 nk = L.s.r[13];
+      if (nk == 0u) {
+        fine = false;  // the crossing lies outside the list: cannot happen
+      } else {
+        klo = L.s.r[14];
+        idlo = L.s.r[15];
+        W = L.s.r64[14];
+        A = W;
+        kept = nat + nk;
+      }
+      lds_sync();
     } else {
       // the exact boundary among the listed tokens (in id order in L.u.fin.ent)
       Held h;
@@ -2321,7 +2367,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     why = mass_row<DT>(a, p, row, c, ch, L);
   }
   if (why == kNotLast) return;
-  if (why != 0u) resolve_single<DT>(a, row, why, L);
+  if (why != 0u) resolve_single<DT>(kernel_args(), row, why, L);
   reset_row(a, row);
 }
 
