@@ -140,7 +140,10 @@ __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   p.k = a.top_k ? (int)uni((u32)gld(a.top_k + row)) : 0;
   const bool topk_on = p.k > 0 && p.k < a.V;
   p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? unif(gld(a.top_p + row)) : 1.0f;
-  p.topp = p.tp < 1.0f;
+  // the flags from the bit patterns, by scalar integer compares (a float compare
+  // runs on the vector unit and leaves a 64-bit lane mask in scalar registers)
+  const u32 tpb = __float_as_uint(p.tp);
+  p.topp = (int)tpb < 0x3f800000 && (tpb & 0x7fffffffu) <= 0x7f800000u;  // tp < 1 (not NaN)
   p.mp = a.min_p ? unif(gld(a.min_p + row)) : 0.0f;
   p.rep = a.rep ? unif(gld(a.rep + row)) : 1.0f;
   p.rrep = 1.0f / p.rep;
@@ -150,12 +153,14 @@ __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   if (p.hlen > a.H) p.hlen = a.H;
   if (p.hlen < 0) p.hlen = 0;
   p.hist = a.hist ? a.hist + (size_t)row * a.H : nullptr;
-  p.pen = p.hist != nullptr && p.hlen > 0 && (p.rep != 1.0f || p.pres != 0.0f || p.freq != 0.0f);
+  p.pen = p.hist != nullptr && p.hlen > 0 &&
+          (__float_as_uint(p.rep) != 0x3f800000u || (__float_as_uint(p.pres) & 0x7fffffffu) != 0u ||
+           (__float_as_uint(p.freq) & 0x7fffffffu) != 0u);  // rep != 1, pres != 0 or freq != 0
   p.u = a.uniforms ? unif(gld(a.uniforms + row)) : 0.0f;
   if (!(p.u >= 0.0f)) p.u = 0.0f;
   if (p.u >= 1.0f) p.u = __uint_as_float(0x3f7fffffu);
   p.kind = greedy ? kKindGreedy : (topk_on ? (p.k <= kTopkMax ? kKindTopK : kKindSingle) : kKindMass);
-  p.t_one = p.T == 1.0f;
+  p.t_one = __float_as_uint(p.T) == 0x3f800000u;  // T == 1
   p.rT = 1.0f / p.T;
   return p;
 }
@@ -334,18 +339,45 @@ __device__ __forceinline__ float elem_zc(const Chunk<DT>& ch, const RowP& p, con
   }
   return z;
 }
+// The row's penalty flag as a compile-time constant: f(Tag<p.pen>()), so that
+// the per-element loops test it once.
+template <bool B>
+struct Tag {
+  static constexpr bool value = B;
+};
+template <typename F>
+__device__ __forceinline__ void with_pen(bool pen, F&& f) {
+  if (pen)
+    f(Tag<true>{});
+  else
+    f(Tag<false>{});
+}
+// elem_zc with the penalty flag known at compile time.
+template <bool PEN, int DT>
+__device__ __forceinline__ float elem_zt(const Chunk<DT>& ch, const RowP& p, const u32 (&pw)[kEPT / 2], int j, int e) {
+  float z = ch.raw(j, e);
+  if constexpr (PEN) {
+    const int i = j * Chunk<DT>::VL + e;
+    const u32 n = (pw[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+    if (n) z = apply_penalty(z, n, p.rep, p.rrep, p.pres, p.freq);
+  }
+  return z;
+}
 // Keys of q = z / T for every element (0 for NaN and invalid elements).
 template <int DT, typename LT>
 __device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, const LT& L, int c, u32 (&kq)[kEPT]) {
-  u32 pw[kEPT / 2];
-  if (p.pen) chunk_counts(L, ch, c, pw);
+  with_pen(p.pen, [&](auto pen) {
+    constexpr bool PEN = decltype(pen)::value;
+    u32 pw[kEPT / 2] = {};
+    if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-  for (int j = 0; j < Chunk<DT>::J; ++j)
+    for (int j = 0; j < Chunk<DT>::J; ++j)
 #pragma unroll
-    for (int e = 0; e < Chunk<DT>::VL; ++e) {
-      const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-      kq[j * Chunk<DT>::VL + e] = skey(q);  // 0 past V (NaN padding)
-    }
+      for (int e = 0; e < Chunk<DT>::VL; ++e) {
+        const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+        kq[j * Chunk<DT>::VL + e] = skey(q);  // 0 past V (NaN padding)
+      }
+  });
 }
 
 // ---------------------------------------------------------------- row synchronisation
@@ -1630,16 +1662,19 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
     // z keys
   u32 kz[E];
   u32 m = 0;
-  u32 pw[kEPT / 2];
-  if (p.pen) chunk_counts(L, ch, c, pw);
+  with_pen(p.pen, [&](auto pen) {
+    constexpr bool PEN = decltype(pen)::value;
+    u32 pw[kEPT / 2] = {};
+    if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-  for (int j = 0; j < J; ++j)
+    for (int j = 0; j < J; ++j)
 #pragma unroll
-    for (int e = 0; e < VL; ++e) {
-      const u32 kx = skey(elem_zc(ch, p, pw, j, e));  // 0 past V (NaN padding)
-      kz[j * VL + e] = kx;
-      m = max(m, kx);
-    }
+      for (int e = 0; e < VL; ++e) {
+        const u32 kx = skey(elem_zt<PEN>(ch, p, pw, j, e));  // 0 past V (NaN padding)
+        kz[j * VL + e] = kx;
+        m = max(m, kx);
+      }
+  });
   if (p.pen) lds_sync();
   QS_TR(2);
   // quota of the chunk and of each wave
@@ -2335,16 +2370,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 
   if (p.kind == kKindGreedy) {
     u64 best = 0;
-    u32 pw[kEPT / 2];
-    if (p.pen) chunk_counts(L, ch, c, pw);
+    with_pen(p.pen, [&](auto pen) {
+      constexpr bool PEN = decltype(pen)::value;
+      u32 pw[kEPT / 2] = {};
+      if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-    for (int j = 0; j < J; ++j)
+      for (int j = 0; j < J; ++j)
 #pragma unroll
-      for (int e = 0; e < VL; ++e) {
-        const float z = elem_zc(ch, p, pw, j, e);
-        const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
-        best = pk > best ? pk : best;
-      }
+        for (int e = 0; e < VL; ++e) {
+          const float z = elem_zt<PEN>(ch, p, pw, j, e);
+          const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+          best = pk > best ? pk : best;
+        }
+    });
     if (p.pen) lds_sync();
     best = block_max64(best, L.s);
     if (threadIdx.x == 0) stc(&sl[c].a, best);
