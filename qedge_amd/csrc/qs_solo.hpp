@@ -112,16 +112,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   if (p.kind == kKindGreedy) {
     u64 best = 0;
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
-      u32 pw[kEPT / 2];
-      if (p.pen) chunk_counts(L, ch, c, pw);
+      with_pen(p.pen, [&](auto pen) {
+        constexpr bool PEN = decltype(pen)::value;
+        u32 pw[kEPT / 2] = {};
+        if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-      for (int j = 0; j < J; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const float z = elem_zc(ch, p, pw, j, e);
-          const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
-          best = pk > best ? pk : best;
-        }
+          for (int e = 0; e < VL; ++e) {
+            const float z = elem_zt<PEN>(ch, p, pw, j, e);
+            const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+            best = pk > best ? pk : best;
+          }
+      });
     });
     best = block_max64(best, L.s);
     const u32 id = 0xffffffffu - (u32)best;
@@ -156,20 +159,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     gbest = 0xffffffffu;  // every z NaN: the first id
   } else {
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
-      u32 pw[kEPT / 2];
-      if (p.pen) chunk_counts(L, ch, c, pw);
+      with_pen(p.pen, [&](auto pen) {
+        constexpr bool PEN = decltype(pen)::value;
+        u32 pw[kEPT / 2] = {};
+        if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-      for (int j = 0; j < J; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const float z = elem_zc(ch, p, pw, j, e);
-          const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));  // 0 past V (NaN padding)
-          kmax = max(kmax, k);
-          kmin = k ? min(kmin, k) : kmin;
-          nnan += k ? 1u : 0u;
-          const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
-          gbest = pk > gbest ? pk : gbest;
-        }
+          for (int e = 0; e < VL; ++e) {
+            const float z = elem_zt<PEN>(ch, p, pw, j, e);
+            const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));  // 0 past V (NaN padding)
+            kmax = max(kmax, k);
+            kmin = k ? min(kmin, k) : kmin;
+            nnan += k ? 1u : 0u;
+            const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+            gbest = pk > gbest ? pk : gbest;
+          }
+      });
     });
     u32 nk = ~kmin;
     block_max2(kmax, nk, L.s);
@@ -193,15 +199,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       const int bl = bitlen(hi - lo);
       const int sh = bl > 8 ? bl - 8 : 0;
       solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
-        u32 pw[kEPT / 2];
-        if (p.pen) chunk_counts(L, ch, c, pw);
+        with_pen(p.pen, [&](auto pen) {
+          constexpr bool PEN = decltype(pen)::value;
+          u32 pw[kEPT / 2] = {};
+          if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-        for (int j = 0; j < J; ++j)
+          for (int j = 0; j < J; ++j)
 #pragma unroll
-          for (int e = 0; e < VL; ++e) {
-            const u32 k = skey(qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one));
-            if (k >= lo && k <= hi && k) atomicAdd(&L.hc[(hi - k) >> sh], 1u);
-          }
+            for (int e = 0; e < VL; ++e) {
+              const u32 k = skey(qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one));
+              if (k >= lo && k <= hi && k) atomicAdd(&L.hc[(hi - k) >> sh], 1u);
+            }
+        });
       });
       lds_sync();
       const int b = threadIdx.x;
@@ -245,25 +254,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   u64 S = 0;
   u32 nz = 0;
   solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
-    u32 pw[kEPT / 2];
-    if (p.pen) chunk_counts(L, ch, c, pw);
+    with_pen(p.pen, [&](auto pen) {
+      constexpr bool PEN = decltype(pen)::value;
+      u32 pw[kEPT / 2] = {};
+      if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      u64 sj = 0;
+      for (int j = 0; j < J; ++j) {
+        u64 sj = 0;
 #pragma unroll
-      for (int e = 0; e < VL; ++e) {
-        const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-        const u32 k = skey(q);
-        const u32 x = wpk(q, k);
-        const u64 w = wunpack(x);
-        sj += w;
-        nz += x ? 1u : 0u;
-        if (p.topp && x) atomicAdd(&L.mh[mass_bin(q, k, qs, kmax, br.mb0)], w);
+        for (int e = 0; e < VL; ++e) {
+          const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+          const u32 k = skey(q);
+          const u32 x = wpk(q, k);
+          const u64 w = wunpack(x);
+          sj += w;
+          nz += x ? 1u : 0u;
+          if (p.topp && x) atomicAdd(&L.mh[mass_bin(q, k, qs, kmax, br.mb0)], w);
+        }
+        const u64 sw = wave_sum64(sj);
+        if (lane_id() == 0) L.seg[(c * kWaves + wave_id()) * J + j] = sw;
+        S += lane_id() == 0 ? sw : 0ull;
       }
-      const u64 sw = wave_sum64(sj);
-      if (lane_id() == 0) L.seg[(c * kWaves + wave_id()) * J + j] = sw;
-      S += lane_id() == 0 ? sw : 0ull;
-    }
+    });
   });
   block_sum2(S, nz, L.s);
   u64 W = S, A = 0, wt = 0;
@@ -286,23 +298,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         const int bl = bitlen(hi - lo);
         const int sh = bl > 8 ? bl - 8 : 0;
         solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
-          u32 pw[kEPT / 2];
-          if (p.pen) chunk_counts(L, ch, c, pw);
+          with_pen(p.pen, [&](auto pen) {
+            constexpr bool PEN = decltype(pen)::value;
+            u32 pw[kEPT / 2] = {};
+            if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-          for (int j = 0; j < J; ++j)
+            for (int j = 0; j < J; ++j)
 #pragma unroll
-            for (int e = 0; e < VL; ++e) {
-              const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-              const u32 k = skey(q);
-              if (k && k >= br.lo && k <= br.hi) {
-                const u64 w = wunpack(wpk(q, k));
-                if (w) {
-                  const u32 b = key_bin(k, lo, hi, sh);
-                  atomicAdd(&L.mh[b], w);
-                  atomicAdd(&L.hc[b], 1u);
+              for (int e = 0; e < VL; ++e) {
+                const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+                const u32 k = skey(q);
+                if (k && k >= br.lo && k <= br.hi) {
+                  const u64 w = wunpack(wpk(q, k));
+                  if (w) {
+                    const u32 b = key_bin(k, lo, hi, sh);
+                    atomicAdd(&L.mh[b], w);
+                    atomicAdd(&L.hc[b], 1u);
+                  }
                 }
               }
-            }
+          });
         });
         lds_sync();
       }
@@ -385,39 +400,42 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     lds_sync();
     u32 nzb = 0;  // tokens at or below the bracket with nonzero weight
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
-      u32 pw[kEPT / 2];
-      if (p.pen) chunk_counts(L, ch, c, pw);
+      with_pen(p.pen, [&](auto pen) {
+        constexpr bool PEN = decltype(pen)::value;
+        u32 pw[kEPT / 2] = {};
+        if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        u64 sub = 0;
-        u32 ties = 0;
+        for (int j = 0; j < J; ++j) {
+          u64 sub = 0;
+          u32 ties = 0;
 #pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const float q = qdiv(elem_zc(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-          const u32 k = skey(q);
-          if (!k) continue;
-          const int side = bracket_side(br, k);
-          if (side == 0) continue;
-          const u64 w = wunpack(wpk(q, k));
-          sub += w;
-          nzb += w ? 1u : 0u;
-          if (side == 1 && w) {
-            if (single) {
-              ++ties;
-            } else {
-              const u32 slot = atomicAdd(&L.nlist, 1u);
-              if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)ch.id(j, e);
+          for (int e = 0; e < VL; ++e) {
+            const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+            const u32 k = skey(q);
+            if (!k) continue;
+            const int side = bracket_side(br, k);
+            if (side == 0) continue;
+            const u64 w = wunpack(wpk(q, k));
+            sub += w;
+            nzb += w ? 1u : 0u;
+            if (side == 1 && w) {
+              if (single) {
+                ++ties;
+              } else {
+                const u32 slot = atomicAdd(&L.nlist, 1u);
+                if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)ch.id(j, e);
+              }
             }
           }
+          const u64 sw = wave_sum64(sub);
+          const u32 tw = wave_sum(ties);
+          if (lane_id() == 0) {
+            const int sg = (c * kWaves + wave_id()) * J + j;
+            L.seg[sg] -= sw;
+            L.segt[sg] = tw;
+          }
         }
-        const u64 sw = wave_sum64(sub);
-        const u32 tw = wave_sum(ties);
-        if (lane_id() == 0) {
-          const int sg = (c * kWaves + wave_id()) * J + j;
-          L.seg[sg] -= sw;
-          L.segt[sg] = tw;
-        }
-      }
+      });
     });
     nzb = block_sum(nzb, L.s);
     const u32 na = nz - nzb;  // tokens above the bracket with nonzero weight
