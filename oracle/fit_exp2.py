@@ -2,7 +2,7 @@
 
 The contract's weight rule evaluates 2^f for f in [0, 1) as a degree-6
 polynomial with c0 = 1 in fp32 fused multiply-adds (oracle/contract.c QS_P2,
-qedge_amd/csrc/qs_contract.hpp).  The coefficients c1..c6 come from this fit:
+qedge_amd/csrc/qs_device.hpp).  The coefficients c1..c6 come from this fit:
 
   * 4097 Chebyshev nodes on [0, 1];
   * least squares on the relative error (2^f - 1 - sum c_j f^j) / 2^f, with
