@@ -2075,6 +2075,13 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     u64* hr = row_hist(a, row);
     for (int i = threadIdx.x; i < kRounds * kNB; i += kThreads) stc(&hr[i], 0ull);
   }
+  // without top-p: the chunks' masses and counts, loaded before the status so
+  // that both come back in one round trip (G <= kMaxG < kThreads: one per thread)
+  u64 cmb = 0, cmc = 0;
+  if (!p.topp && (int)threadIdx.x < a.G) {
+    cmb = ldc(&sl[threadIdx.x].b);
+    cmc = ldc(&sl[threadIdx.x].c);
+  }
   const u32 st = ldc(&sy->status);
   if (st != 0u || kstar == 0u) return st ? st : kStIncomplete;
   // per-chunk kept masses and tie counts in L.cmass / L.cties
@@ -2088,11 +2095,12 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   };
   auto wf = [&](u32 key) -> u64 { return wunpack(wpk(key)); };
   if (!p.topp) {
+    static_assert(kMaxG <= kThreads, "one chunk per thread");
     u32 nzt = 0;
-    for (int cc = threadIdx.x; cc < a.G; cc += kThreads) {
-      L.cmass[cc] = ldc(&sl[cc].b);
-      nzt += (u32)ldc(&sl[cc].c);
-      L.cties[cc] = 0u;
+    if ((int)threadIdx.x < a.G) {
+      L.cmass[threadIdx.x] = cmb;
+      nzt = (u32)cmc;
+      L.cties[threadIdx.x] = 0u;
     }
     kept = block_sum(nzt, L.s);
   } else {
