@@ -282,6 +282,40 @@ def test_special_values_in_top_keys(gpu, dtype):
     _check(xx, dtype, gpu, T, P, K, u=u)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ties_at_the_one_wave_finishers(gpu, dtype):
+    """Tie groups where the one-wave finishers draw their lines, every row on
+    its fast path:
+      0  k = 10 with 100 tokens at the k-th value: the sorted finisher keeps 64
+         and hands the row to the general one (ties may go on past the 64);
+      1  k = 20 with 40 tokens at the k-th value: the sorted finisher keeps all;
+      2  top-k off, top-p 0.5 inside a group of 30 tied tokens (a short list);
+      3  top-k off, top-p 0.7 across two tie groups near the top;
+      4  k = 63 with 64 tied tokens at the top;
+      5  k = 3 with 5 tied tokens (ties kept), top-p 0.9."""
+    rng = np.random.default_rng(23)
+    B, V = 6, 100000
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    ties = rng.choice(V, 100, replace=False)
+    x[0, ties] = 9.0
+    x[1, ties[:40]] = 9.0
+    x[2, ties[:30]] = 12.0
+    x[3, ties[:12]] = 12.0
+    x[3, ties[12:20]] = 11.5
+    x[4, ties[:64]] = 8.0
+    x[5, ties[:5]] = 8.0
+    xx = W.bf16_bits(x) if dtype == "bf16" else x
+    T = np.array([1.0, 0.8, 1.0, 0.9, 1.0, 0.7], np.float32)
+    P = np.array([0.9, 0.8, 0.5, 0.7, 0.95, 0.9], np.float32)
+    K = np.array([10, 20, 0, 0, 63, 3], np.int32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] tie groups at the finishers {dtype}", flush=True)
+    paths = []
+    _check(xx, dtype, gpu, T, P, K, u=u, paths=paths)
+    path, why = paths
+    assert not np.any(why), f"rows fell back: {np.nonzero(why)[0].tolist()} (reasons {why.tolist()})"
+
+
 @pytest.mark.parametrize("B,V,dtype", [(1, 248320, "bf16"), (2, 2048 * 7 + 100, "bf16"), (3, 600001, "bf16"),
                                        (12, 8192 * 5 + 300, "f32")])
 def test_chunk_layouts_and_sparse_last_chunks(gpu, B, V, dtype):
