@@ -256,10 +256,11 @@ __device__ __forceinline__ void block_excl2(u32& c, u64& m, Scratch& s, u32* cto
 
 // Sampling key: orderable bits, NaN lowest (0), -0 == +0.
 __device__ __forceinline__ u32 skey(float z) {
-  if (z != z) return 0u;
-  if (z == 0.0f) z = 0.0f;
-  const u32 u = __float_as_uint(z);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  // z + 0 turns -0 into +0 (round to nearest) and keeps every other value,
+  // denormals included; then the sign-magnitude bits become an unsigned order
+  const u32 u = __float_as_uint(z + 0.0f);
+  const u32 k = u ^ ((u32)((int)u >> 31) | 0x80000000u);
+  return (z != z) ? 0u : k;
 }
 // Greedy key: NaN highest.
 __device__ __forceinline__ u32 gkey(float z) { return (z != z) ? 0xffffffffu : skey(z); }
