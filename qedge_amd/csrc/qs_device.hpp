@@ -325,10 +325,10 @@ __device__ __forceinline__ u32 wpack_of(float q, u32 k, float qs, u32 ks, int SH
   return live ? ((u32)(s + 64) << 24) | m : 0u;
 }
 __device__ __forceinline__ u64 wunpack(u32 wp) {
+  // wp == 0 has m == 0; a live weight has -23 <= s <= 39, so m << s < 2^63
   const u64 m = wp & 0xffffffu;
   const int s = (int)(wp >> 24) - 64;
-  const u64 w = s >= 0 ? (m << s) : (m >> (-s));
-  return wp ? w : 0ull;
+  return (m << (s > 0 ? s : 0)) >> (s < 0 ? min(-s, 63) : 0);
 }
 __device__ __forceinline__ u64 weight_of(float q, u32 k, float qs, u32 ks, int SH) {
   return wunpack(wpack_of(q, k, qs, ks, SH));
