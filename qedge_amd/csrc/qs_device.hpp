@@ -312,16 +312,19 @@ constexpr float kL2E = 0x1.715476p+0f;  // fp32(log2 e)
 // ks), SH = 40 - ceil(log2 V), packed in 32 bits as ((s + 64) << 24) | M with
 // w = M << s (s >= 0) or M >> -s; 0 when the weight is 0.  Branch-free.
 __device__ __forceinline__ u32 wpack_of(float q, u32 k, float qs, u32 ks, int SH) {
+  // Dead tokens are computed through and masked at the end: NaN q has key 0, and
+  // with q* finite (or d = 0) every other y is a number or -inf, so s > -24
+  // (which implies y >= -64 for SH <= 40) decides; floor(y) is clamped before
+  // its conversion so that the conversion stays in range.
   const float d = (k == ks) ? 0.0f : q - qs;
   const float y = d * kL2E;
-  bool live = (y >= -64.0f) && (k != 0u);  // NaN q has key 0; a NaN y fails the compare
-  const float fl = __builtin_floorf(live ? y : 0.0f);
-  const float f = (live ? y : 0.0f) - fl;
+  const float fl = __builtin_floorf(y);
+  const float f = y - fl;
   float p = exp2_poly(f);
-  p = fminf(fmaxf(p, 1.0f), __uint_as_float(0x3fffffffu));
+  p = __builtin_amdgcn_fmed3f(p, 1.0f, __uint_as_float(0x3fffffffu));
   const u32 m = 0x800000u | (__float_as_uint(p) & 0x7fffffu);
-  const int s = (int)fl + SH;
-  live = live && s > -24;
+  const int s = (int)fmaxf(fl, -128.0f) + SH;
+  const bool live = k != 0u && s > -24;
   return live ? ((u32)(s + 64) << 24) | m : 0u;
 }
 __device__ __forceinline__ u64 wunpack(u32 wp) {
