@@ -1527,6 +1527,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
 struct MassBins {
   float x0, x1, s1, s2;
   int n1;
+  float c2;  // n1 - x1 * s2: the second segment is c2 + x * s2
 };
 static_assert(kNB <= 256, "a bin index fits a byte");
 constexpr float kXMax = 44.5f;  // y = -x * log2(e) < -64 past it: weight 0
@@ -1546,12 +1547,15 @@ __device__ __forceinline__ MassBins mass_bins_first(float D) {
     m.s1 = D > 0x1p-60f ? (float)kNB / D : 0.0f;  // no spread: every token in bin 0
     m.s2 = 0.0f;
   }
+  m.c2 = (float)m.n1 - m.x1 * m.s2;
   return m;
 }
+// The two segments make a concave map (s1 >= s2: 16 bins per unit, then at most
+// 64 / 4), so the bin position is the smaller of the two lines.
 __device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, const MassBins& m) {
   const float d = (k == ks) ? 0.0f : q - qs;
   const float x = -d - m.x0;
-  const float f = x < m.x1 ? x * m.s1 : (float)m.n1 + (x - m.x1) * m.s2;
+  const float f = fminf(x * m.s1, __builtin_fmaf(x, m.s2, m.c2));
   return min((u32)kNB - 1u, (u32)fmaxf(0.0f, f));
 }
 // x at the far edge of bin b
@@ -1579,6 +1583,7 @@ __device__ __forceinline__ MassBins mass_bins_split(const MassBins& m, u32 b) {
   n.x1 = w > 0.0f ? w : 0.0f;
   n.s1 = w > 0x1p-60f ? (float)kNB / w : 0.0f;
   n.s2 = 0.0f;
+  n.c2 = (float)kNB;
   return n;
 }
 // One wave re-reads segment s and returns, to every lane, the id of the token
