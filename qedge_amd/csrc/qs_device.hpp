@@ -270,6 +270,48 @@ __device__ __forceinline__ float f_of_key(u32 k) {
 }
 __device__ __forceinline__ float bf16_to_f32(u32 h) { return __uint_as_float(h << 16); }
 
+// ---------------------------------------------------------------- 16-bit keys of bf16 logits, two per register
+//
+// For streaming passes over bf16 logits without penalties (z is the logit
+// itself): the h key of a bf16 bit pattern x is (x ^ (sign ? 0xffff : 0x8000))
+// + 0x7f mod 2^16, computed for both halves of a register with packed 16-bit
+// operations.  It orders like the values, with the NaNs wrapped below -inf:
+// NaNs in [0, 0xfd], -inf 0xfe, finite values and +inf in [0xff, 0xffff]; -0
+// (0x807e) sits one below +0 (0x807f), so code that needs them equal compares
+// through key_of_h, which maps both to the key of +0 only after skey().
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef short ss2 __attribute__((ext_vector_type(2)));
+constexpr u32 kHNegInf = 0xfeu;  // h key of -inf; every h key below it is a NaN
+__device__ __forceinline__ u32 hkey2(u32 x) {
+  const u32 s = __builtin_bit_cast(u32, __builtin_bit_cast(ss2, x) >> (ss2)15);
+  return __builtin_bit_cast(u32, __builtin_bit_cast(us2, x ^ (s | 0x80008000u)) + (us2)0x7f);
+}
+// The sampling key (skey without the -0 fold: -0 gives 0x7fffffff) of the value
+// with h key h; 0 for NaN.
+__device__ __forceinline__ u32 key_of_h(u32 h) {
+  if (h < kHNegInf) return 0u;
+  const u32 k = (h - 0x7fu) & 0xffffu;
+  return k >= 0x8000u ? (k << 16) : ((k << 16) | 0xffffu);
+}
+__device__ __forceinline__ u32 pk_max_u16(u32 a, u32 b) {
+  return __builtin_bit_cast(u32, __builtin_elementwise_max(__builtin_bit_cast(us2, a), __builtin_bit_cast(us2, b)));
+}
+__device__ __forceinline__ u32 pk_min_u16(u32 a, u32 b) {
+  return __builtin_bit_cast(u32, __builtin_elementwise_min(__builtin_bit_cast(us2, a), __builtin_bit_cast(us2, b)));
+}
+__device__ __forceinline__ u32 pk_add_u16(u32 a, u32 b) {
+  return __builtin_bit_cast(u32, __builtin_bit_cast(us2, a) + __builtin_bit_cast(us2, b));
+}
+// max(a - b, 0) per half.  Written as the instruction itself: in source form
+// the compiler turns min(sub_sat(a, b), 1) into compares and selects per half.
+__device__ __forceinline__ u32 pk_sub_sat_u16(u32 a, u32 b) {
+  u32 r;
+  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// Per half: 1 when h >= t + 1, else 0 (t1 holds t in both halves).
+__device__ __forceinline__ u32 pk_above(u32 h, u32 t1) { return pk_min_u16(pk_sub_sat_u16(h, t1), 0x00010001u); }
+
 // z / b for a row-constant b with r = 1 / b (correctly rounded): Markstein's
 // correction of q0 = z * r by the exact residual fma(-q0, b, z).  It equals the
 // correctly rounded z / b whenever div_fast_ok holds (|z| and |q0| in

@@ -391,6 +391,14 @@ __device__ __forceinline__ u32 arrive(u32* ctr, Scratch& s) {
   lds_sync();
   return s.r[0];
 }
+// The same counting n (the chunks this workgroup served).
+__device__ __forceinline__ u32 arrive_n(u32* ctr, u32 n, Scratch& s) {
+  wait_mem();
+  lds_sync();
+  if (threadIdx.x == 0) s.r[0] = addc(ctr, n);
+  lds_sync();
+  return s.r[0];
+}
 // Thread 0 waits until *ctr >= target (or the row failed / the limit passed).
 // Returns true when the target was reached, to every thread.
 __device__ __forceinline__ bool wait_count(const Args& a, int row, const u32* ctr, u32 target, Scratch& s) {
@@ -1655,15 +1663,111 @@ __device__ __forceinline__ u64* seg_base(const Args& a, int row) { return list_b
 
 // ---------------------------------------------------------------- the streaming kernel
 
-// Streaming and (in the row's last workgroup) finishing of a top-k row.
-// Returns kNotLast in the other workgroups, else 0 or a reason to resolve the
-// row by the exact single-workgroup path.
-template <int DT>
-__device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int row, const int c, Chunk<DT>& ch,
-                                        Lds& L) {
-  constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
+// The chunk's candidate quota: nw waves hold logits of the row; each keeps
+// at least kw tokens and the chunk at least kc, kc = mu + 4 sqrt(mu) + 2 for the
+// mu = k * kCH / V tokens of the row's top k that a chunk holds on average.
+// (A heuristic: it sets how many candidates the chunk writes, never the result;
+// hardware reciprocal and square root suffice.)
+struct Quota {
+  int nw, kc, kw, jw;
+};
+__device__ __forceinline__ Quota topk_quota(const Args& a, const RowP& p, int c) {
+  Quota q;
+  const int vin = min(kCH, a.V - c * kCH);
+  q.nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
+  const float mu = (float)p.k * (float)kCH * __builtin_amdgcn_rcpf((float)a.V);
+  q.kc = (int)uni((u32)(int)ceilf(mu + 4.0f * __builtin_amdgcn_sqrtf(mu) + 2.0f));
+  q.kc = min(q.kc, p.k);
+  q.kw = min(64, max(1, (q.kc + q.nw - 1) / q.nw));
+  q.jw = min(q.nw, (q.kc + q.kw - 1) / q.kw);
+  return q;
+}
+// The chunk threshold on 16-bit keys m16 (each thread's largest): tw, the
+// kw-th largest per-thread maximum of each wave (lanes holding a maximum >= tw:
+// at least kw), then tau, the jw-th largest tw over the waves, so that jw waves
+// hold kw tokens >= tau each.  Uses L.s.v[][4].
+__device__ __forceinline__ u32 topk_tau16(u32 m16, const Quota& q, Lds& L) {
+  u32 tw = 0;
+  for (int b = 15; b >= 0; --b) {
+    const u32 cand = tw | (1u << b);
+    if ((int)popc64(__ballot(m16 >= cand)) >= q.kw) tw = cand;
+  }
+  if (lane_id() == 0) L.s.v[wave_id()][4] = wave_id() < q.nw ? tw : 0u;
+  lds_sync();
+  u32 tv[kWaves];
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) tv[i] = uni(L.s.v[i][4]);
+  static_assert(kWaves == 8, "sorting network for 8 waves");
+  constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3},
+                              {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+  for (int i = 0; i < 19; ++i) {
+    const u32 x = tv[net[i][0]], y = tv[net[i][1]];
+    tv[net[i][0]] = max(x, y);
+    tv[net[i][1]] = min(x, y);
+  }
+  u32 tau = tv[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) tau = (i == q.jw - 1) ? tv[i] : tau;
+  return tau;
+}
+
+// What a top-k chunk's streaming leaves for topk_tail.
+struct TkOut {
+  u32 n, below, zmax, tau32;
+};
+// The slot of a top-k chunk after its region is written (n candidates, n =
+// 0xffffffff for an overflow), by thread 0: below is the largest z key the
+// chunk left out (an upper bound suffices: a larger one can only send the row
+// to the exact path), zmax the chunk's largest z key, tau32 the z key at and
+// above which every token of the chunk is in its region.
+__device__ __forceinline__ void topk_slot(const Args& a, const RowP& p, const int row, const int c, const TkOut& t) {
+  Slot* sl = row_slots(a, row);
+  const u32 qmax = t.zmax ? skey(qdiv(f_of_key(t.zmax), p.T, p.rT, p.t_one)) : 0u;
+  const u32 qlow = skey(qdiv(f_of_key(t.tau32), p.T, p.rT, p.t_one));
+  stc(&sl[c].a, ((u64)t.below << 32) | t.n);
+  stc(&sl[c].d, ((u64)qmax << 32) | qlow);
+}
+
+// The arrival of a workgroup that wrote nch chunks' slots of a top-k row, and in
+// the row's last workgroup the gather and the finish.  Returns kNotLast in the
+// other workgroups, else 0 or a reason to resolve the row by the exact path.
+__device__ __forceinline__ u32 topk_last(const Args& a, const RowP& p, const int row, const int c, Lds& L, u32 nch) {
   RowSync* sy = &a.sync[row];
   Slot* sl = row_slots(a, row);
+  const int R = a.R;
+  QS_TR(5);
+  if (arrive_n(&sy->arrive, nch, L.s) != (u32)a.G - nch) return kNotLast;
+  QS_TR(6);
+  // ---- the row's last workgroup: gather and finish
+  u32 mx[3];
+  const u32 tot = gather_lds(a, row_data(a, row), R, [&](int cc, u32(&v)[3]) -> u32 {
+    const u64 x = ldc(&sl[cc].a), d = ldc(&sl[cc].d);
+    v[0] = (u32)(x >> 32);  // largest z key left out
+    v[1] = (u32)(d >> 32);  // largest q key
+    v[2] = ~(u32)d;         // the complement of the q key of the chunk's threshold
+    return (u32)x;
+  }, L, mx);
+  QS_TR(7);
+  const u32 below_max = mx[0], qmax = mx[1], qlow = ~mx[2];
+  QS_TR(8);
+  u32 why = 0u;
+  bool done = false;
+  if (tot == 0xffffffffu)
+    why = kStOverflow;
+  else if (finish_topk(a, p, row, L, tot, qmax, qlow, below_max, c))
+    done = true;
+  else
+    why = kStIncomplete;
+  QS_TR(14);
+  return done ? 0u : why;
+}
+
+// The streaming part of a top-k row: the chunk's candidates to its region.
+template <int DT>
+__device__ __forceinline__ TkOut topk_row(const Args& a, const RowP& p, const int row, const int c, Chunk<DT>& ch,
+                                        Lds& L) {
+  constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
     // z keys
   u32 kz[E];
   u32 m = 0;
@@ -1682,47 +1786,8 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
   });
   if (p.pen) lds_sync();
   QS_TR(2);
-  // quota of the chunk and of each wave
-  const int vin = min(kCH, a.V - c * kCH);
-  const int nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
-  const float mu = (float)p.k * (float)kCH / (float)a.V;
-  int kc = (int)ceilf(mu + 4.0f * sqrtf(mu) + 2.0f);
-  kc = min(kc, p.k);
-  const int kw = min(64, max(1, (kc + nw - 1) / nw));
-  // tw: the kw-th largest per-thread maximum of the wave, to the top 16 key bits
-  // (lanes holding a maximum >= tw: at least kw); tau: the jw-th largest tw over
-  // the waves, jw = ceil(kc / kw), so that jw waves hold kw tokens >= tau each
-  u32 tw = 0;
-  {
-    const u32 m16 = m >> 16;
-    for (int b = 15; b >= 0; --b) {
-      const u32 cand = tw | (1u << b);
-      if ((int)popc64(__ballot(m16 >= cand)) >= kw) tw = cand;
-    }
-    tw <<= 16;
-  }
-  if (lane_id() == 0) L.s.v[wave_id()][4] = wave_id() < nw ? tw : 0u;
-  lds_sync();
-  const int jw = min(nw, (kc + kw - 1) / kw);
-  u32 tau;
-  {
-    u32 tv[kWaves];
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) tv[i] = uni(L.s.v[i][4]);
-    static_assert(kWaves == 8, "sorting network for 8 waves");
-    constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3},
-                                {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
-#pragma unroll
-    for (int i = 0; i < 19; ++i) {
-      const u32 x = tv[net[i][0]], y = tv[net[i][1]];
-      tv[net[i][0]] = max(x, y);
-      tv[net[i][1]] = min(x, y);
-    }
-    tau = tv[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; ++i) tau = (i == jw - 1) ? tv[i] : tau;
-  }
-  tau = max(tau, 1u);
+  const Quota qt = topk_quota(a, p, c);
+  u32 tau = max(topk_tau16(m >> 16, qt, L) << 16, 1u);
   QS_TR(3);
   const int R = a.R;
   u32 n = 0, below = 0, zmax = 0;
@@ -1799,38 +1864,263 @@ __device__ __forceinline__ u32 topk_row(const Args& a, const RowP& p, const int 
     QS_TR(4);
     break;
   }
-  // the q keys of the chunk's largest and of tau
-  if (threadIdx.x == 0) {
-    const u32 qmax = zmax ? skey(qdiv(f_of_key(zmax), p.T, p.rT, p.t_one)) : 0u;
-    const u32 qlow = skey(qdiv(f_of_key(tau), p.T, p.rT, p.t_one));
-    stc(&sl[c].a, ((u64)below << 32) | n);
-    stc(&sl[c].d, ((u64)qmax << 32) | qlow);
+  return TkOut{n, below, zmax, tau};
+}
+
+// Top-k and greedy rows of bf16 logits without penalties: a workgroup serves
+// kCPW consecutive chunks (chunk c0 = kCPW * i and the next kCPW - 1 of the row),
+// all in step, on h keys (two per register), so that the row parameters, the
+// exchanges between waves and the arrival are paid once per kCPW chunks.
+constexpr int kCPW = 2;
+
+// The bf16 bits of the value with h key h (h >= kHNegInf; -0 for 0x807e).
+__device__ __forceinline__ u32 bf16_of_h(u32 h) {
+  const u32 k = (h - 0x7fu) & 0xffffu;
+  return k >= 0x8000u ? (k & 0x7fffu) : (~k & 0xffffu);
+}
+
+// h keys of a chunk's logits: hk[j * 4 + w] holds the keys of word w of vector
+// j (elements 2w and 2w + 1 of the vector); returns the thread's largest.
+__device__ __forceinline__ u32 chunk_hkeys(const Chunk<QS_DTYPE_BF16>& ch, u32 (&hk)[kEPT / 2]) {
+  u32 m2 = 0;
+#pragma unroll
+  for (int j = 0; j < Chunk<QS_DTYPE_BF16>::J; ++j) {
+    const uint4 v = ch.v[j];
+    hk[j * 4 + 0] = hkey2(v.x);
+    hk[j * 4 + 1] = hkey2(v.y);
+    hk[j * 4 + 2] = hkey2(v.z);
+    hk[j * 4 + 3] = hkey2(v.w);
   }
-  QS_TR(5);
-  if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return kNotLast;
-  QS_TR(6);
-  // ---- the row's last workgroup: gather and finish
-  u32 mx[3];
-  const u32 tot = gather_lds(a, row_data(a, row), R, [&](int cc, u32(&v)[3]) -> u32 {
-    const u64 x = ldc(&sl[cc].a), d = ldc(&sl[cc].d);
-    v[0] = (u32)(x >> 32);  // largest z key left out
-    v[1] = (u32)(d >> 32);  // largest q key
-    v[2] = ~(u32)d;         // the complement of the q key of the chunk's threshold
-    return (u32)x;
-  }, L, mx);
-  QS_TR(7);
-  const u32 below_max = mx[0], qmax = mx[1], qlow = ~mx[2];
-  QS_TR(8);
-  u32 why = 0u;
-  bool done = false;
-  if (tot == 0xffffffffu)
-    why = kStOverflow;
-  else if (finish_topk(a, p, row, L, tot, qmax, qlow, below_max, c))
-    done = true;
-  else
-    why = kStIncomplete;
-  QS_TR(14);
-  return done ? 0u : why;
+#pragma unroll
+  for (int i = 0; i < kEPT / 2; ++i) m2 = pk_max_u16(m2, hk[i]);
+  return max(m2 & 0xffffu, m2 >> 16);
+}
+
+// The streaming part of a top-k row for chunks c0 .. c0 + nch - 1 (nch <=
+// kCPW): each chunk's candidates to its region and its slot.  Per logit pair one
+// key, one maximum and one count step; the tokens at or above a chunk's
+// threshold are written by the threads that hold them (a few per chunk); the
+// largest key a chunk leaves out is bounded by its threshold's predecessor.
+__device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int row, const int c0, const int nch,
+                                        const Chunk<QS_DTYPE_BF16> (&ch)[kCPW], Lds& L) {
+  constexpr int NW = kEPT / 2, WPV = 4, J = Chunk<QS_DTYPE_BF16>::J, NC = kCPW;
+  const int R = a.R;
+  u32 hk[NC][NW];
+  u32 m[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) m[k] = chunk_hkeys(ch[k], hk[k]);
+  QS_TRA(2);
+  // thresholds: per chunk tw (each wave's kw-th largest per-thread maximum),
+  // then tau, the jw-th largest tw over the waves, all chunks in one exchange.
+  // Every chunk but the row's last has the same quota.
+  const Quota qf = topk_quota(a, p, 0), ql = topk_quota(a, p, a.G - 1);
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int kw = c0 + k == a.G - 1 ? ql.kw : qf.kw;
+    u32 tw = 0;
+    for (int b = 15; b >= 0; --b) {
+      const u32 cand = tw | (1u << b);
+      if ((int)popc64(__ballot(m[k] >= cand)) >= kw) tw = cand;
+    }
+    const int nw = c0 + k == a.G - 1 ? ql.nw : qf.nw;
+    if (lane_id() == 0) L.s.v[wave_id()][4 + k] = wave_id() < nw ? tw : 0u;
+  }
+  lds_sync();
+  u32 tau[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    // the jw-th largest of the eight by a sorting network (vector registers:
+    // the same values in every lane)
+    u32 tv[kWaves];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) tv[i] = L.s.v[i][4 + k];
+    constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3},
+                                {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+    for (int i = 0; i < 19; ++i) {
+      const u32 x = tv[net[i][0]], y = tv[net[i][1]];
+      tv[net[i][0]] = max(x, y);
+      tv[net[i][1]] = min(x, y);
+    }
+    const int jw = c0 + k == a.G - 1 ? ql.jw : qf.jw;
+    u32 t = tv[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) t = (i == jw - 1) ? tv[i] : t;
+    tau[k] = max(t, kHNegInf);  // never a NaN
+  }
+  QS_TRA(3);
+  // counts per (chunk, vector) and their offsets in id order (wave, j, lane, e);
+  // the chunk's total and largest key, all chunks in one exchange
+  u32 pos[NC][J], n[NC], zmax[NC];
+  u32 has = 0;  // bit k * J + j: this thread holds a candidate in vector j of chunk k
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    has = 0;
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const u32 t1 = (tau[k] - 1u) * 0x10001u;
+      u32 tot = 0;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        u32 acc = 0;
+#pragma unroll
+        for (int w = 0; w < WPV; ++w) acc = pk_add_u16(acc, pk_above(hk[k][j * WPV + w], t1));
+        const u32 cn = (acc & 0xffffu) + (acc >> 16);
+        has |= cn != 0u ? 1u << (k * J + j) : 0u;
+        const u32 inc = wave_incl_scan(cn);
+        pos[k][j] = tot + inc - cn;
+        tot += readlane(inc, 63);
+      }
+      const u32 wm = wave_max(m[k]);
+      if (lane_id() == 0) L.s.w[wave_id()][k] = ((u64)tot << 32) | wm;
+    }
+    lds_sync();
+    bool over = false;
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      u32 woff = 0, nk = 0, zk = 0;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) {
+        const u64 x = L.s.w[i][k];
+        const u32 ti = (u32)(x >> 32);
+        woff += i < wave_id() ? ti : 0u;
+        nk += ti;
+        zk = max(zk, (u32)x);
+      }
+      n[k] = uni(nk);
+      zmax[k] = uni(zk);
+#pragma unroll
+      for (int j = 0; j < J; ++j) pos[k][j] += woff;
+      over = over || (k < nch && n[k] > (u32)R);
+    }
+    if (!over) break;
+    lds_sync();  // the exchange is read: it may be written again
+    if (attempt == 1) break;
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+      if (n[k] > (u32)R) tau[k] += 1u;  // ties at tau overflowed the region: strictly above it
+  }
+  // each candidate straight to its chunk's region, as (key of q << 32 | id), by
+  // the threads that hold one, in id order (j, word, half)
+  const int base = ch[0].base;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    if (k >= nch || n[k] > (u32)R) continue;
+    u64* reg = row_data(a, row) + (size_t)(c0 + k) * R;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (has & (1u << (k * J + j))) {
+        u32 ps = pos[k][j];
+#pragma unroll
+        for (int w = 0; w < WPV; ++w) {
+          const u32 hw = hk[k][j * WPV + w];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const u32 h = (hw >> (16 * hf)) & 0xffffu;
+            if (h >= tau[k]) {
+              const float q = qdiv(bf16_to_f32(bf16_of_h(h)), p.T, p.rT, p.t_one);
+              const int id = base + k * kCH + j * 64 * Chunk<QS_DTYPE_BF16>::VL + 2 * w + hf;
+              stc(&reg[ps], ((u64)skey(q) << 32) | (u32)id);
+              ++ps;
+            }
+          }
+        }
+      }
+    }
+  }
+  QS_TRA(4);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+      if (k < nch) {
+        const u32 nk = n[k] > (u32)R ? 0xffffffffu : n[k];
+        topk_slot(a, p, row, c0 + k, TkOut{nk, key_of_h(tau[k] - 1u), key_of_h(zmax[k]), key_of_h(tau[k])});
+      }
+  }
+}
+
+// The same for a greedy row: each chunk's (greedy key, ~id) to its slot.  The g
+// key h - 0xfe (mod 2^16) puts the NaNs above +inf; the first index of the
+// chunk's largest is found by the threads that hold it (with -0 equal to +0 and
+// every NaN equal).  Logits past V (NaN padding) are masked to the lowest key.
+__device__ __forceinline__ void greedy_pk(const Args& a, const int row, const int c0, const int nch,
+                                          const Chunk<QS_DTYPE_BF16> (&ch)[kCPW], Lds& L) {
+  constexpr int NW = kEPT / 2, WPV = 4, J = Chunk<QS_DTYPE_BF16>::J, NC = kCPW;
+  constexpr u32 kGOff = 0xff02ff02u;  // -0xfe in both halves
+  u32 gk[NC][NW];
+  u32 gm[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    chunk_hkeys(ch[k], gk[k]);
+    const bool last = c0 + k == a.G - 1;  // the chunk that may run past V
+    u32 m2 = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int w = 0; w < WPV; ++w) {
+        u32 g = pk_add_u16(gk[k][j * WPV + w], kGOff);
+        if (last) {
+          const u32 lo = ch[k].valid(j, 2 * w) ? 0xffffu : 0u, hi = ch[k].valid(j, 2 * w + 1) ? 0xffff0000u : 0u;
+          g &= lo | hi;
+        }
+        gk[k][j * WPV + w] = g;
+        m2 = pk_max_u16(m2, g);
+      }
+    gm[k] = max(m2 & 0xffffu, m2 >> 16);
+  }
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const u32 wmx = wave_max(gm[k]);
+    if (lane_id() == 0) L.s.v[wave_id()][4 + k] = wmx;
+  }
+  lds_sync();
+  u32 G[NC], first[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    G[k] = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) G[k] = max(G[k], L.s.v[i][4 + k]);
+    // the keys equal to the largest: every NaN; -0 and +0 (g 0x7f80, 0x7f81)
+    const u32 lo = G[k] >= 0xff02u ? 0xff02u : (G[k] == 0x7f81u ? 0x7f80u : G[k]);
+    u32 id = 0xffffffffu;
+    if (gm[k] >= lo) {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int w = 0; w < WPV; ++w)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const u32 g = (gk[k][j * WPV + w] >> (16 * hf)) & 0xffffu;
+            const u32 i = (u32)ch[k].id(j, 2 * w + hf);
+            id = (g >= lo && i < id) ? i : id;
+          }
+    }
+    first[k] = wave_min(id);
+  }
+  lds_sync();  // the maxima are read: the exchange may be written again
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) L.s.v[wave_id()][4 + k] = first[k];
+  }
+  lds_sync();
+  if (threadIdx.x == 0) {
+    Slot* sl = row_slots(a, row);
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+      if (k < nch) {
+        u32 id = 0xffffffffu;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) id = min(id, L.s.v[i][4 + k]);
+        u32 key;
+        if (G[k] >= 0xff02u) {
+          key = 0xffffffffu;  // NaN
+        } else {
+          key = key_of_h((G[k] + 0xfeu) & 0xffffu);
+          if (key == 0x7fffffffu) key = 0x80000000u;  // -0 as +0
+        }
+        // a chunk of padding only has no id: key 0 loses to every real logit
+        stc(&sl[c0 + k].a, id == 0xffffffffu ? 0ull : (((u64)key << 32) | (0xffffffffu - id)));
+      }
+  }
 }
 
 // A top-k-off row: keys, the row barrier, weights, the bracket rounds, and (in
@@ -2363,6 +2653,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   QS_TR(0);
   Chunk<DT> ch;
   load_chunk<DT>(a, row, c, ch);
+  // bf16 rows: the workgroups of chunks c = 0 mod kCPW also load the next
+  // kCPW - 1 chunks, which they serve for top-k and greedy rows without penalties
+  const bool lead = c % kCPW == 0;
   int pre[kHistPre];  // the row's first history ids, loaded beside the chunk
   if (a.hist) {
     const int* h = a.hist + (size_t)row * a.H;
@@ -2381,26 +2674,46 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   (void)J;
   (void)VL;
 
+  u32 nch = 1;  // chunks served by this workgroup
+  bool packed = false;
+  if constexpr (DT == QS_DTYPE_BF16) {
+    if (!p.pen && (p.kind == kKindGreedy || p.kind == kKindTopK)) {
+      if (!lead) return;  // served by the workgroup of chunk c - c % kCPW
+      nch = (u32)min(kCPW, a.G - c);
+      Chunk<QS_DTYPE_BF16> chx[kCPW];
+      chx[0] = ch;
+#pragma unroll
+      for (int k = 1; k < kCPW; ++k) load_chunk<QS_DTYPE_BF16>(a, row, c + k, chx[k]);
+      if (p.kind == kKindGreedy)
+        greedy_pk(a, row, c, (int)nch, chx, L);
+      else
+        topk_pk(a, p, row, c, (int)nch, chx, L);
+      packed = true;
+    }
+  }
+
   if (p.kind == kKindGreedy) {
-    u64 best = 0;
-    with_pen(p.pen, [&](auto pen) {
-      constexpr bool PEN = decltype(pen)::value;
-      u32 pw[kEPT / 2] = {};
-      if constexpr (PEN) chunk_counts(L, ch, c, pw);
+    if (!packed) {
+      u64 best = 0;
+      with_pen(p.pen, [&](auto pen) {
+        constexpr bool PEN = decltype(pen)::value;
+        u32 pw[kEPT / 2] = {};
+        if constexpr (PEN) chunk_counts(L, ch, c, pw);
 #pragma unroll
-      for (int j = 0; j < J; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const float z = elem_zt<PEN>(ch, p, pw, j, e);
-          const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
-          best = pk > best ? pk : best;
-        }
-    });
-    if (p.pen) lds_sync();
-    best = block_max64(best, L.s);
-    if (threadIdx.x == 0) stc(&sl[c].a, best);
+          for (int e = 0; e < VL; ++e) {
+            const float z = elem_zt<PEN>(ch, p, pw, j, e);
+            const u64 pk = ((u64)(ch.valid(j, e) ? gkey(z) : 0u) << 32) | (0xffffffffu - (u32)ch.id(j, e));
+            best = pk > best ? pk : best;
+          }
+      });
+      if (p.pen) lds_sync();
+      best = block_max64(best, L.s);
+      if (threadIdx.x == 0) stc(&sl[c].a, best);
+    }
     QS_TR(2);
-    if (arrive(&sy->arrive, L.s) != (u32)a.G - 1u) return;
+    if (arrive_n(&sy->arrive, nch, L.s) != (u32)a.G - nch) return;
     QS_TR(3);
     finish_greedy(a, p, row, L);
     reset_row(a, row);
@@ -2410,7 +2723,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 
   u32 why;
   if (p.kind == kKindTopK) {
-    why = topk_row<DT>(a, p, row, c, ch, L);
+    if (!packed) {
+      const TkOut t = topk_row<DT>(a, p, row, c, ch, L);
+      if (threadIdx.x == 0) topk_slot(a, p, row, c, t);
+    }
+    why = topk_last(a, p, row, c, L, nch);
   } else if (p.kind == kKindSingle) {
     if (p.pen) lds_sync();
     why = arrive(&sy->arrive, L.s) == (u32)a.G - 1u ? kWhyLargeK : kNotLast;
