@@ -62,6 +62,21 @@ template <typename T>
 __device__ __forceinline__ void gst(T* p, T v) {
   *gp(p) = v;
 }
+// A value the same for the whole launch (row parameters, the dispatch order),
+// read through the scalar data cache: a scalar load, counted apart from the
+// vector loads of the logits, so that waiting for it does not wait for them.
+// Read-only data only: nothing the launch writes.
+#if defined(__HIP_DEVICE_COMPILE__)
+template <typename T>
+__device__ __forceinline__ T sld(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+#else
+template <typename T>
+__device__ __forceinline__ T sld(const T* p) {
+  return *p;
+}
+#endif
 template <typename T>
 __device__ __forceinline__ T ldc(const T* p) {
   return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

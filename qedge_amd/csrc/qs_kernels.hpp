@@ -135,28 +135,28 @@ __device__ __forceinline__ float unif(float v) { return __uint_as_float(uni(__fl
 __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   RowP p;
   row = (int)uni((u32)row);
-  p.T = a.temperature ? unif(gld(a.temperature + row)) : 0.0f;
+  p.T = a.temperature ? unif(sld(a.temperature + row)) : 0.0f;
   const bool greedy = (a.flags & QS_FLAG_ALL_GREEDY) || (p.T <= 1e-5f);
-  p.k = a.top_k ? (int)uni((u32)gld(a.top_k + row)) : 0;
+  p.k = a.top_k ? (int)uni((u32)sld(a.top_k + row)) : 0;
   const bool topk_on = p.k > 0 && p.k < a.V;
-  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? unif(gld(a.top_p + row)) : 1.0f;
+  p.tp = ((a.flags & QS_FLAG_USE_TOP_P) && a.top_p) ? unif(sld(a.top_p + row)) : 1.0f;
   // the flags from the bit patterns, by scalar integer compares (a float compare
   // runs on the vector unit and leaves a 64-bit lane mask in scalar registers)
   const u32 tpb = __float_as_uint(p.tp);
   p.topp = (int)tpb < 0x3f800000 && (tpb & 0x7fffffffu) <= 0x7f800000u;  // tp < 1 (not NaN)
-  p.mp = a.min_p ? unif(gld(a.min_p + row)) : 0.0f;
-  p.rep = a.rep ? unif(gld(a.rep + row)) : 1.0f;
+  p.mp = a.min_p ? unif(sld(a.min_p + row)) : 0.0f;
+  p.rep = a.rep ? unif(sld(a.rep + row)) : 1.0f;
   p.rrep = 1.0f / p.rep;
-  p.pres = a.pres ? unif(gld(a.pres + row)) : 0.0f;
-  p.freq = a.freq ? unif(gld(a.freq + row)) : 0.0f;
-  p.hlen = a.hist ? (a.hist_len ? (int)uni((u32)gld(a.hist_len + row)) : a.H) : 0;
+  p.pres = a.pres ? unif(sld(a.pres + row)) : 0.0f;
+  p.freq = a.freq ? unif(sld(a.freq + row)) : 0.0f;
+  p.hlen = a.hist ? (a.hist_len ? (int)uni((u32)sld(a.hist_len + row)) : a.H) : 0;
   if (p.hlen > a.H) p.hlen = a.H;
   if (p.hlen < 0) p.hlen = 0;
   p.hist = a.hist ? a.hist + (size_t)row * a.H : nullptr;
   p.pen = p.hist != nullptr && p.hlen > 0 &&
           (__float_as_uint(p.rep) != 0x3f800000u || (__float_as_uint(p.pres) & 0x7fffffffu) != 0u ||
            (__float_as_uint(p.freq) & 0x7fffffffu) != 0u);  // rep != 1, pres != 0 or freq != 0
-  p.u = a.uniforms ? unif(gld(a.uniforms + row)) : 0.0f;
+  p.u = a.uniforms ? unif(sld(a.uniforms + row)) : 0.0f;
   if (!(p.u >= 0.0f)) p.u = 0.0f;
   if (p.u >= 1.0f) p.u = __uint_as_float(0x3f7fffffu);
   p.kind = greedy ? kKindGreedy : (topk_on ? (p.k <= kTopkMax ? kKindTopK : kKindSingle) : kKindMass);
@@ -2648,14 +2648,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   __shared__ Lds L;
   constexpr int E = kEPT, J = Chunk<DT>::J, VL = Chunk<DT>::VL;
   const int c = blockIdx.x;
-  const int row = (int)uni(a.order ? (u32)gld(a.order + blockIdx.y) : blockIdx.y);
+  const int row = (int)uni(a.order ? (u32)sld(a.order + blockIdx.y) : blockIdx.y);
   if ((unsigned)row >= (unsigned)a.B) return;  // row_order must be a permutation of [0, B)
   QS_TR(0);
+  // bf16 rows: the workgroup of chunk c = 0 mod kCPW (the lead) serves the next
+  // kCPW - 1 chunks too for top-k and greedy rows without penalties.  Without
+  // histories (no row has penalties) the other workgroups load their chunk once
+  // the row parameters show that it is theirs; with histories they load it at
+  // once (most such rows have penalties and need every workgroup).
+  const bool lead = DT != QS_DTYPE_BF16 || c % kCPW == 0;
+  const bool eager = lead || a.hist != nullptr;
   Chunk<DT> ch;
-  load_chunk<DT>(a, row, c, ch);
-  // bf16 rows: the workgroups of chunks c = 0 mod kCPW also load the next
-  // kCPW - 1 chunks, which they serve for top-k and greedy rows without penalties
-  const bool lead = c % kCPW == 0;
+  if (eager) load_chunk<DT>(a, row, c, ch);
   int pre[kHistPre];  // the row's first history ids, loaded beside the chunk
   if (a.hist) {
     const int* h = a.hist + (size_t)row * a.H;
@@ -2666,6 +2670,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     }
   }
   const RowP p = row_params(a, row);
+  const bool packed_row = DT == QS_DTYPE_BF16 && !p.pen && (p.kind == kKindGreedy || p.kind == kKindTopK);
+  if (!lead && packed_row) return;  // served by the lead
+  if (!eager) load_chunk<DT>(a, row, c, ch);
   RowSync* sy = &a.sync[row];
   Slot* sl = row_slots(a, row);
   if (p.pen) pen_build_pre(p, c, L, pre);
@@ -2677,8 +2684,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   u32 nch = 1;  // chunks served by this workgroup
   bool packed = false;
   if constexpr (DT == QS_DTYPE_BF16) {
-    if (!p.pen && (p.kind == kKindGreedy || p.kind == kKindTopK)) {
-      if (!lead) return;  // served by the workgroup of chunk c - c % kCPW
+    if (packed_row) {
       nch = (u32)min(kCPW, a.G - c);
       Chunk<QS_DTYPE_BF16> chx[kCPW];
       chx[0] = ch;
