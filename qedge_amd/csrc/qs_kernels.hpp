@@ -878,9 +878,12 @@ __device__ __forceinline__ void finish_greedy(const Args& a, const RowP& p, int 
 // values mx[] whose workgroup maxima are returned in mx (threads past the lists
 // hold zeros).  Returns the total, or 0xffffffff when a list overflowed or the
 // total exceeds kFCap.  Needs G <= kThreads.
-template <typename CF>
+struct NoXf {
+  __device__ __forceinline__ u64 operator()(u64 e) const { return e; }
+};
+template <typename CF, typename XF = NoXf>
 __device__ __forceinline__ u32 gather_lds(const Args& a, const u64* base, int stride, CF&& cnt_of, Lds& L,
-                                          u32 (&mx)[3]) {
+                                          u32 (&mx)[3], XF xf = XF()) {
   constexpr int M = kFCap / kThreads;
   const int G = a.G;
   const int lp = 31 - __clz(min(stride, kFCap / G));
@@ -930,13 +933,13 @@ __device__ __forceinline__ u32 gather_lds(const Args& a, const u64* base, int st
   for (int m = 0; m < M; ++m) {
     const int f = (int)threadIdx.x + m * kThreads;
     const int c = f >> lp, i = f & (P - 1);
-    if (c < G && (u32)i < L.cties[c]) L.u.fin.ent[L.coff[c] + i] = spec[m];
+    if (c < G && (u32)i < L.cties[c]) L.u.fin.ent[L.coff[c] + i] = xf(spec[m]);
   }
   if (any_long) {
     for (int c = 0; c < G; ++c) {  // lists longer than P
       const u32 n_c = L.cties[c];
       for (u32 i = (u32)P + threadIdx.x; i < n_c; i += kThreads)
-        L.u.fin.ent[L.coff[c] + i] = ldc(base + (size_t)c * stride + i);
+        L.u.fin.ent[L.coff[c] + i] = xf(ldc(base + (size_t)c * stride + i));
     }
   }
   lds_sync();
@@ -1732,7 +1735,10 @@ __device__ __forceinline__ void topk_slot(const Args& a, const RowP& p, const in
 // The arrival of a workgroup that wrote nch chunks' slots of a top-k row, and in
 // the row's last workgroup the gather and the finish.  Returns kNotLast in the
 // other workgroups, else 0 or a reason to resolve the row by the exact path.
-__device__ __forceinline__ u32 topk_last(const Args& a, const RowP& p, const int row, const int c, Lds& L, u32 nch) {
+// With zk the regions and the slots hold z keys (the rows of topk_pk): the
+// entries become keys of q as they are gathered, the chunk extremes after.
+__device__ __forceinline__ u32 topk_last(const Args& a, const RowP& p, const int row, const int c, Lds& L, u32 nch,
+                                         bool zk) {
   RowSync* sy = &a.sync[row];
   Slot* sl = row_slots(a, row);
   const int R = a.R;
@@ -1741,15 +1747,23 @@ __device__ __forceinline__ u32 topk_last(const Args& a, const RowP& p, const int
   QS_TR(6);
   // ---- the row's last workgroup: gather and finish
   u32 mx[3];
-  const u32 tot = gather_lds(a, row_data(a, row), R, [&](int cc, u32(&v)[3]) -> u32 {
+  auto cnt_of = [&](int cc, u32(&v)[3]) -> u32 {
     const u64 x = ldc(&sl[cc].a), d = ldc(&sl[cc].d);
     v[0] = (u32)(x >> 32);  // largest z key left out
-    v[1] = (u32)(d >> 32);  // largest q key
-    v[2] = ~(u32)d;         // the complement of the q key of the chunk's threshold
+    v[1] = (u32)(d >> 32);  // largest key (of q, or of z with zk)
+    v[2] = ~(u32)d;         // the complement of the key of the chunk's threshold
     return (u32)x;
-  }, L, mx);
+  };
+  auto qkey = [&](u32 zkey) -> u32 { return skey(qdiv(f_of_key(zkey), p.T, p.rT, p.t_one)); };
+  u32 tot;
+  if (zk)
+    tot = gather_lds(a, row_data(a, row), R, cnt_of, L, mx,
+                     [&](u64 e) -> u64 { return ((u64)qkey((u32)(e >> 32)) << 32) | (u32)e; });
+  else
+    tot = gather_lds(a, row_data(a, row), R, cnt_of, L, mx);
   QS_TR(7);
-  const u32 below_max = mx[0], qmax = mx[1], qlow = ~mx[2];
+  const u32 below_max = mx[0];
+  const u32 qmax = zk ? (mx[1] ? qkey(mx[1]) : 0u) : mx[1], qlow = zk ? qkey(~mx[2]) : ~mx[2];
   QS_TR(8);
   u32 why = 0u;
   bool done = false;
@@ -1913,40 +1927,53 @@ __device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int 
   // thresholds: per chunk tw (each wave's kw-th largest per-thread maximum),
   // then tau, the jw-th largest tw over the waves, all chunks in one exchange.
   // Every chunk but the row's last has the same quota.
-  const Quota qf = topk_quota(a, p, 0), ql = topk_quota(a, p, a.G - 1);
+  const Quota qf = topk_quota(a, p, 0);
+  const Quota ql = c0 + NC > a.G - 1 ? topk_quota(a, p, a.G - 1) : qf;
+  u32 tw[NC];
 #pragma unroll
-  for (int k = 0; k < NC; ++k) {
-    const int kw = c0 + k == a.G - 1 ? ql.kw : qf.kw;
-    u32 tw = 0;
-    for (int b = 15; b >= 0; --b) {
-      const u32 cand = tw | (1u << b);
-      if ((int)popc64(__ballot(m[k] >= cand)) >= kw) tw = cand;
+  for (int k = 0; k < NC; ++k) tw[k] = 0;
+  for (int b = 15; b >= 0; --b) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int kw = c0 + k == a.G - 1 ? ql.kw : qf.kw;
+      const u32 cand = tw[k] | (1u << b);
+      if ((int)popc64(__ballot(m[k] >= cand)) >= kw) tw[k] = cand;
     }
-    const int nw = c0 + k == a.G - 1 ? ql.nw : qf.nw;
-    if (lane_id() == 0) L.s.v[wave_id()][4 + k] = wave_id() < nw ? tw : 0u;
+  }
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int nw = c0 + k == a.G - 1 ? ql.nw : qf.nw;
+      L.s.v[wave_id()][4 + k] = wave_id() < nw ? tw[k] : 0u;
+    }
   }
   lds_sync();
+  // the jw-th largest of the eight: lane k * 8 + i holds wave i's value of
+  // chunk k; a bitonic sort of each group of eight lanes (descending) by DPP
   u32 tau[NC];
+  {
+    const int l = (int)lane_id();
+    const int kk = min(l >> 3, NC - 1);
+    u32 v = L.s.v[l & 7][4 + kk];
+    // compare-exchange with the partner lane; the lane in the lower half of the
+    // pair's block keeps the larger (a bitonic network with mirrored merges)
+#define QS_CX(CTRL, lowbit)                                  \
+  {                                                          \
+    const u32 o = dpp_mov<CTRL, 0xF>(v);                     \
+    v = (l & (lowbit)) == 0 ? max(v, o) : min(v, o);         \
+  }
+    QS_CX(0xB1, 1)   // quad_perm [1,0,3,2]: partner l ^ 1
+    QS_CX(0x1B, 2)   // quad_perm [3,2,1,0]: partner l ^ 3
+    QS_CX(0xB1, 1)
+    QS_CX(0x141, 4)  // row_half_mirror: partner 7 - l within the 8
+    QS_CX(0x4E, 2)   // quad_perm [2,3,0,1]: partner l ^ 2
+    QS_CX(0xB1, 1)
+#undef QS_CX
 #pragma unroll
-  for (int k = 0; k < NC; ++k) {
-    // the jw-th largest of the eight by a sorting network (vector registers:
-    // the same values in every lane)
-    u32 tv[kWaves];
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) tv[i] = L.s.v[i][4 + k];
-    constexpr int net[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3},
-                                {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
-#pragma unroll
-    for (int i = 0; i < 19; ++i) {
-      const u32 x = tv[net[i][0]], y = tv[net[i][1]];
-      tv[net[i][0]] = max(x, y);
-      tv[net[i][1]] = min(x, y);
+    for (int k = 0; k < NC; ++k) {
+      const int jw = c0 + k == a.G - 1 ? ql.jw : qf.jw;
+      tau[k] = max(readlane(v, k * 8 + jw - 1), kHNegInf);  // never a NaN
     }
-    const int jw = c0 + k == a.G - 1 ? ql.jw : qf.jw;
-    u32 t = tv[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; ++i) t = (i == jw - 1) ? tv[i] : t;
-    tau[k] = max(t, kHNegInf);  // never a NaN
   }
   QS_TRA(3);
   // counts per (chunk, vector) and their offsets in id order (wave, j, lane, e);
@@ -2017,9 +2044,8 @@ __device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int 
           for (int hf = 0; hf < 2; ++hf) {
             const u32 h = (hw >> (16 * hf)) & 0xffffu;
             if (h >= tau[k]) {
-              const float q = qdiv(bf16_to_f32(bf16_of_h(h)), p.T, p.rT, p.t_one);
               const int id = base + k * kCH + j * 64 * Chunk<QS_DTYPE_BF16>::VL + 2 * w + hf;
-              stc(&reg[ps], ((u64)skey(q) << 32) | (u32)id);
+              stc(&reg[ps], ((u64)key_of_h(h) << 32) | (u32)id);
               ++ps;
             }
           }
@@ -2028,13 +2054,19 @@ __device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int 
     }
   }
   QS_TRA(4);
-  if (threadIdx.x == 0) {
+  // slots with z keys (topk_last converts them)
+  if (threadIdx.x < (u32)nch) {
+    Slot* sl = row_slots(a, row);
+    u32 nk = 0, t = 0, zm = 0;
 #pragma unroll
     for (int k = 0; k < NC; ++k)
-      if (k < nch) {
-        const u32 nk = n[k] > (u32)R ? 0xffffffffu : n[k];
-        topk_slot(a, p, row, c0 + k, TkOut{nk, key_of_h(tau[k] - 1u), key_of_h(zmax[k]), key_of_h(tau[k])});
+      if ((int)threadIdx.x == k) {
+        nk = n[k] > (u32)R ? 0xffffffffu : n[k];
+        t = tau[k];
+        zm = zmax[k];
       }
+    stc(&sl[c0 + threadIdx.x].a, ((u64)key_of_h(t - 1u) << 32) | nk);
+    stc(&sl[c0 + threadIdx.x].d, ((u64)key_of_h(zm) << 32) | key_of_h(t));
   }
 }
 
@@ -2733,7 +2765,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       const TkOut t = topk_row<DT>(a, p, row, c, ch, L);
       if (threadIdx.x == 0) topk_slot(a, p, row, c, t);
     }
-    why = topk_last(a, p, row, c, L, nch);
+    why = topk_last(a, p, row, c, L, nch, packed);
   } else if (p.kind == kKindSingle) {
     if (p.pen) lds_sync();
     why = arrive(&sy->arrive, L.s) == (u32)a.G - 1u ? kWhyLargeK : kNotLast;
