@@ -79,6 +79,7 @@ struct Args {
   long long row_stride;
   int B, V, G, R, SH, H;
   int vec_ok;
+  float kmu;  // kCH / V: the share of a row's top k that a chunk holds on average
   u32 flags, spin_limit;
   const float* temperature;
   const float* top_p;
@@ -1678,11 +1679,14 @@ __device__ __forceinline__ Quota topk_quota(const Args& a, const RowP& p, int c)
   Quota q;
   const int vin = min(kCH, a.V - c * kCH);
   q.nw = min(kWaves, (vin + kWaveSpan - 1) / kWaveSpan);
-  const float mu = (float)p.k * (float)kCH * __builtin_amdgcn_rcpf((float)a.V);
-  q.kc = (int)uni((u32)(int)ceilf(mu + 4.0f * __builtin_amdgcn_sqrtf(mu) + 2.0f));
-  q.kc = min(q.kc, p.k);
-  q.kw = min(64, max(1, (q.kc + q.nw - 1) / q.nw));
-  q.jw = min(q.nw, (q.kc + q.kw - 1) / q.kw);
+  const float mu = (float)p.k * a.kmu;
+  const float kc = ceilf(mu + 4.0f * __builtin_amdgcn_sqrtf(mu) + 2.0f);
+  q.kc = min((int)uni((u32)(int)kc), p.k);
+  // kw = ceil(kc / nw) and jw = ceil(kc / kw): by hardware reciprocals, which
+  // can only round up (one more candidate wave or token, never fewer)
+  const float kcf = (float)q.kc;
+  q.kw = min(64, max(1, (int)uni((u32)(int)ceilf(kcf * __builtin_amdgcn_rcpf((float)q.nw)))));
+  q.jw = min(q.nw, max(1, (int)uni((u32)(int)ceilf(kcf * __builtin_amdgcn_rcpf((float)q.kw)))));
   return q;
 }
 // The chunk threshold on 16-bit keys m16 (each thread's largest): tw, the
@@ -2001,23 +2005,38 @@ __device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int 
       if (lane_id() == 0) L.s.w[wave_id()][k] = ((u64)tot << 32) | wm;
     }
     lds_sync();
+    // lane k * 8 + i takes wave i's (total, largest) of chunk k: prefix sums
+    // and maxima within each group of eight lanes
+    static_assert(NC * kWaves <= 16, "the chunks' groups fit one row of 16 lanes");
     bool over = false;
+    {
+      const int l = (int)lane_id();
+      const u64 x = L.s.w[l & 7][min(l >> 3, NC - 1)];
+      u32 t = (u32)(x >> 32), zm = (u32)x;
+      const int gi = l & 7;  // position within the group
+      // inclusive scan and running maximum over the group (row_shr within
+      // the row of 16; contributions from the group below are masked)
+      u32 s1 = dpp_mov<0x111, 0xF>(t), z1 = dpp_mov<0x111, 0xF>(zm);
+      t += gi >= 1 ? s1 : 0u;
+      zm = gi >= 1 ? max(zm, z1) : zm;
+      s1 = dpp_mov<0x112, 0xF>(t);
+      z1 = dpp_mov<0x112, 0xF>(zm);
+      t += gi >= 2 ? s1 : 0u;
+      zm = gi >= 2 ? max(zm, z1) : zm;
+      s1 = dpp_mov<0x114, 0xF>(t);
+      z1 = dpp_mov<0x114, 0xF>(zm);
+      t += gi >= 4 ? s1 : 0u;
+      zm = gi >= 4 ? max(zm, z1) : zm;
+      const u32 incl = t, own = (u32)(x >> 32);
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
-      u32 woff = 0, nk = 0, zk = 0;
+      for (int k = 0; k < NC; ++k) {
+        n[k] = readlane(incl, k * 8 + 7);
+        zmax[k] = readlane(zm, k * 8 + 7);
+        const u32 woff = readlane(incl - own, k * 8 + wave_id());
 #pragma unroll
-      for (int i = 0; i < kWaves; ++i) {
-        const u64 x = L.s.w[i][k];
-        const u32 ti = (u32)(x >> 32);
-        woff += i < wave_id() ? ti : 0u;
-        nk += ti;
-        zk = max(zk, (u32)x);
+        for (int j = 0; j < J; ++j) pos[k][j] += woff;
+        over = over || (k < nch && n[k] > (u32)R);
       }
-      n[k] = uni(nk);
-      zmax[k] = uni(zk);
-#pragma unroll
-      for (int j = 0; j < J; ++j) pos[k][j] += woff;
-      over = over || (k < nch && n[k] > (u32)R);
     }
     if (!over) break;
     lds_sync();  // the exchange is read: it may be written again

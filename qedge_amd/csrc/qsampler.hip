@@ -160,6 +160,7 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   a.G = L.G;
   a.R = L.R;
   a.SH = L.SH;
+  a.kmu = (float)kCH / (float)V;
   a.H = H;
   const size_t esz = logits_dtype == QS_DTYPE_F32 ? 4 : 2;
   a.vec_ok = ((uintptr_t)logits % 16 == 0) && (((size_t)row_stride * esz) % 16 == 0);
