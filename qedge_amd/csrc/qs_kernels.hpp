@@ -177,6 +177,7 @@ struct FinLds {
   u32 lk[kDirect];          // a bin's keys for the direct resolution
   u64 lw[kDirect];          // and their weights
 };
+constexpr int kSegPre = 1024;  // segment masses a mass row's finisher loads with its lists
 struct Lds {
   union {
     u32 pen[kCH / 2];       // history counts of the chunk, two 16-bit counts per word
@@ -185,6 +186,7 @@ struct Lds {
   } u;
   SelLds sel;               // select histogram (beside the table: the exact pass needs both)
   u64 mh[kNB];              // mass histogram of the chunk
+  u64 segm[kSegPre];        // finisher: every chunk's segment masses (when they fit)
   u64 cmass[kMaxG];         // finisher: per-chunk masses
   u32 cties[kMaxG];         // finisher: per-chunk tie counts
   u32 coff[kMaxG + 1];      // finisher: gathered offsets per chunk
@@ -1919,9 +1921,10 @@ __device__ __forceinline__ u32 chunk_hkeys(const Chunk<QS_DTYPE_BF16>& ch, u32 (
 // key, one maximum and one count step; the tokens at or above a chunk's
 // threshold are written by the threads that hold them (a few per chunk); the
 // largest key a chunk leaves out is bounded by its threshold's predecessor.
+template <int NC>
 __device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int row, const int c0, const int nch,
-                                        const Chunk<QS_DTYPE_BF16> (&ch)[kCPW], Lds& L) {
-  constexpr int NW = kEPT / 2, WPV = 4, J = Chunk<QS_DTYPE_BF16>::J, NC = kCPW;
+                                        const Chunk<QS_DTYPE_BF16>* ch, Lds& L) {
+  constexpr int NW = kEPT / 2, WPV = 4, J = Chunk<QS_DTYPE_BF16>::J;
   const int R = a.R;
   u32 hk[NC][NW];
   u32 m[NC];
@@ -2093,9 +2096,10 @@ __device__ __forceinline__ void topk_pk(const Args& a, const RowP& p, const int 
 // key h - 0xfe (mod 2^16) puts the NaNs above +inf; the first index of the
 // chunk's largest is found by the threads that hold it (with -0 equal to +0 and
 // every NaN equal).  Logits past V (NaN padding) are masked to the lowest key.
+template <int NC>
 __device__ __forceinline__ void greedy_pk(const Args& a, const int row, const int c0, const int nch,
-                                          const Chunk<QS_DTYPE_BF16> (&ch)[kCPW], Lds& L) {
-  constexpr int NW = kEPT / 2, WPV = 4, J = Chunk<QS_DTYPE_BF16>::J, NC = kCPW;
+                                          const Chunk<QS_DTYPE_BF16>* ch, Lds& L) {
+  constexpr int NW = kEPT / 2, WPV = 4, J = Chunk<QS_DTYPE_BF16>::J;
   constexpr u32 kGOff = 0xff02ff02u;  // -0xfe in both halves
   u32 gk[NC][NW];
   u32 gm[NC];
@@ -2193,8 +2197,9 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       if (kr[i]) kmn = min(kmn, kr[i]);
       L.u.kq[i * kThreads + threadIdx.x] = kr[i];
     }
-    kmx = block_max(kmx, L.s);
-    kmn = ~block_max(~kmn, L.s);
+    kmn = ~kmn;
+    block_max2(kmx, kmn, L.s);
+    kmn = ~kmn;
     if (threadIdx.x == 0) stc(&sl[c].a, ((u64)kmx << 32) | kmn);
   }
   QS_TR(2);
@@ -2208,8 +2213,9 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
       kstar = max(kstar, (u32)(v >> 32));
       kmin = min(kmin, (u32)v);
     }
-    kstar = block_max(kstar, L.s);
-    kmin = ~block_max(~kmin, L.s);
+    kmin = ~kmin;
+    block_max2(kstar, kmin, L.s);
+    kmin = ~kmin;
     QS_TR(4);
     if (kstar == 0u) {
       fail_row(a, row, kStIncomplete);  // no weights: resolved alone
@@ -2421,6 +2427,19 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     u64* hr = row_hist(a, row);
     for (int i = threadIdx.x; i < kRounds * kNB; i += kThreads) stc(&hr[i], 0ull);
   }
+  // every chunk's segment masses, when they fit, in the same round trip as the
+  // lists (the owner of the draw is known only after the selection)
+  const int nsg = kWaves * J;
+  const bool segpre = a.G * nsg <= kSegPre;
+  constexpr int kSP = kSegPre / kThreads;
+  u64 spv[kSP];
+  if (segpre) {
+#pragma unroll
+    for (int i = 0; i < kSP; ++i) {
+      const int f = (int)threadIdx.x + i * kThreads;
+      spv[i] = f < a.G * nsg ? ldc(seg_base(a, row) + (size_t)(f / nsg) * kSegMax + (f % nsg)) : 0ull;
+    }
+  }
   // without top-p: the chunks' masses and counts, loaded before the status so
   // that both come back in one round trip (G <= kMaxG < kThreads: one per thread)
   u64 cmb = 0, cmc = 0;
@@ -2429,6 +2448,10 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     cmc = ldc(&sl[threadIdx.x].c);
   }
   const u32 st = ldc(&sy->status);
+  if (segpre) {
+#pragma unroll
+    for (int i = 0; i < kSP; ++i) L.segm[threadIdx.x + i * kThreads] = spv[i];
+  }
   if (st != 0u || kstar == 0u) return st ? st : kStIncomplete;
   // per-chunk kept masses and tie counts in L.cmass / L.cties
   u64 W = 0, wt = 0;
@@ -2638,9 +2661,8 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   // the segment of the owner chunk holding the draw: the segments' masses known
   // before the selection, plus (top-p) the listed tokens kept
   (void)jl;
-  const int nsg = kWaves * J;
   const u64* sg = seg_base(a, row) + (size_t)owner * kSegMax;
-  if ((int)threadIdx.x < nsg) L.cmass[threadIdx.x] = ldc(&sg[threadIdx.x]);
+  if ((int)threadIdx.x < nsg) L.cmass[threadIdx.x] = segpre ? L.segm[owner * nsg + threadIdx.x] : ldc(&sg[threadIdx.x]);
   lds_sync();
   if (p.topp) {
     for (u32 i = threadIdx.x; i < nlist; i += kThreads) {
@@ -2742,9 +2764,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
       for (int k = 1; k < kCPW; ++k) load_chunk<QS_DTYPE_BF16>(a, row, c + k, chx[k]);
       if (p.kind == kKindGreedy)
-        greedy_pk(a, row, c, (int)nch, chx, L);
+        greedy_pk<kCPW>(a, row, c, (int)nch, chx, L);
       else
-        topk_pk(a, p, row, c, (int)nch, chx, L);
+        topk_pk<kCPW>(a, p, row, c, (int)nch, chx, L);
       packed = true;
     }
   }
