@@ -297,13 +297,13 @@ __device__ __forceinline__ float bf16_to_f32(u32 h) { return __uint_as_float(h <
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef short ss2 __attribute__((ext_vector_type(2)));
 constexpr u32 kHNegInf = 0xfeu;  // h key of -inf; every h key below it is a NaN
-__device__ __forceinline__ u32 hkey2(u32 x) {
+__host__ __device__ __forceinline__ u32 hkey2(u32 x) {
   const u32 s = __builtin_bit_cast(u32, __builtin_bit_cast(ss2, x) >> (ss2)15);
   return __builtin_bit_cast(u32, __builtin_bit_cast(us2, x ^ (s | 0x80008000u)) + (us2)0x7f);
 }
 // The sampling key (skey without the -0 fold: -0 gives 0x7fffffff) of the value
 // with h key h; 0 for NaN.
-__device__ __forceinline__ u32 key_of_h(u32 h) {
+__host__ __device__ __forceinline__ u32 key_of_h(u32 h) {
   if (h < kHNegInf) return 0u;
   const u32 k = (h - 0x7fu) & 0xffffu;
   return k >= 0x8000u ? (k << 16) : ((k << 16) | 0xffffu);

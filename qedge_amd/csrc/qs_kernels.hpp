@@ -1894,7 +1894,7 @@ __device__ __forceinline__ TkOut topk_row(const Args& a, const RowP& p, const in
 constexpr int kCPW = 2;
 
 // The bf16 bits of the value with h key h (h >= kHNegInf; -0 for 0x807e).
-__device__ __forceinline__ u32 bf16_of_h(u32 h) {
+__host__ __device__ __forceinline__ u32 bf16_of_h(u32 h) {
   const u32 k = (h - 0x7fu) & 0xffffu;
   return k >= 0x8000u ? (k & 0x7fffu) : (~k & 0xffffu);
 }

@@ -282,6 +282,45 @@ def test_special_values_in_top_keys(gpu, dtype):
     _check(xx, dtype, gpu, T, P, K, u=u)
 
 
+@pytest.mark.parametrize("V", [8192 * 3 + 17, 8192 * 4, 248320])
+def test_bf16_greedy_and_top_k_rows_two_chunks_per_workgroup(gpu, V):
+    """bf16 greedy and top-k rows without penalties (16-bit keys, two chunks per
+    workgroup): NaN as the greedy maximum (first NaN wins), -0 before +0 at the
+    maximum of a non-positive row (the first zero wins), a row of -inf with
+    two finite tokens, an all -inf row (index 0), the maximum in the last,
+    partial or odd chunk (a workgroup serving one chunk), ties at the maximum,
+    and top-k rows beside them with the same layouts."""
+    rng = np.random.default_rng(V % 1009)
+    B = 10
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    x[0, [V // 3, 5, V - 2]] = np.nan                     # first NaN: index 5
+    x[1] = -np.abs(x[1]) - 0.5
+    x[1, [11, 4000, V - 3]] = [-0.0, 0.0, -0.0]           # first zero: 11 (a -0)
+    x[2] = -np.inf
+    x[2, [V - 1, 9]] = [-3.0, -3.0]                       # tie among the only finite tokens
+    x[3] = -np.inf                                        # every token -inf: index 0
+    x[4, V - 1] = 40.0                                    # maximum in the last chunk
+    x[5, [100, V - 100, V // 2]] = 30.0                   # three-way tie at the maximum
+    x[6, V - 4:] = 25.0                                   # top-k inside the last chunk
+    x[7, rng.integers(0, V, 300)] = 0.0
+    x[7, rng.integers(0, V, 300)] = -0.0
+    x[7] = np.minimum(x[7], 0.0)                          # top-k at the zeros
+    xx = W.bf16_bits(x)
+    T = np.array([0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.8, 1.0, 0.9, 0.7], np.float32)
+    P = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 0.9, 0.95, 0.8, 1.0], np.float32)
+    K = np.array([0, 0, 0, 0, 0, 0, 3, 50, 700, 1], np.int32)
+    u = rng.random(B).astype(np.float32)
+    print(f"[edge] bf16 packed rows V={V}", flush=True)
+    for order in (False, True):
+        paths = []
+        ids = _check(xx, "bf16", gpu, T, P, K, u=u, order=order, paths=paths)
+        assert ids[0] == 5 and ids[1] == 11 and ids[2] == 9 and ids[3] == 0 and ids[4] == V - 1 and ids[5] == 100
+        why = paths[1]
+        # (row 7 may take the exact path: -0 and +0 are distinct 16-bit keys, so a
+        # chunk threshold between them leaves a tie with the k-th value out)
+        assert not np.any(why[[6, 8, 9]]), f"top-k rows fell back (reasons {why.tolist()})"
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_ties_at_the_one_wave_finishers(gpu, dtype):
     """Tie groups where the one-wave finishers draw their lines, every row on
