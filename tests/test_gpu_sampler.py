@@ -321,6 +321,30 @@ def test_bf16_greedy_and_top_k_rows_two_chunks_per_workgroup(gpu, V):
         assert not np.any(why[[6, 8, 9]]), f"top-k rows fell back (reasons {why.tolist()})"
 
 
+def test_bf16_batch_with_histories_mixing_penalised_and_plain_rows(gpu):
+    """A bf16 batch with a history matrix where only some rows use penalties:
+    the rows without them take the two-chunk path while every workgroup loads
+    its chunk at once (histories present), the penalised rows the per-chunk
+    path; greedy, top-k and top-k-off rows of both kinds."""
+    rng = np.random.default_rng(97)
+    B, V = 12, 248320
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    xx = W.bf16_bits(x)
+    T = np.array([0.0, 0.8, 1.0, 0.7, 0.0, 0.9, 1.2, 0.6, 0.0, 0.5, 1.0, 0.8], np.float32)
+    P = np.array([1.0, 0.9, 0.95, 0.8, 1.0, 0.7, 1.0, 0.9, 1.0, 0.85, 0.9, 1.0], np.float32)
+    K = np.array([0, 40, 0, 500, 0, 7, 0, 90, 0, 1000, 0, 33], np.int32)
+    rep = np.where(np.arange(B) % 2 == 0, 1.0, 1.15).astype(np.float32)   # even rows: no penalty
+    pres = np.where(np.arange(B) % 2 == 0, 0.0, 0.4).astype(np.float32)
+    freq = np.where(np.arange(B) % 2 == 0, 0.0, 0.2).astype(np.float32)
+    hist = rng.integers(0, V, (B, 1024)).astype(np.int32)
+    top = np.argsort(-x, axis=1)[:, :8]
+    hist[:, :8] = top  # the penalties move the top tokens of the penalised rows
+    u = rng.random(B).astype(np.float32)
+    print("[edge] bf16 histories, penalised and plain rows", flush=True)
+    for order in (False, True):
+        _check(xx, "bf16", gpu, T, P, K, rep, pres, freq, hist, u=u, order=order)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_ties_at_the_one_wave_finishers(gpu, dtype):
     """Tie groups where the one-wave finishers draw their lines, every row on
