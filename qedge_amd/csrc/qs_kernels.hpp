@@ -2271,10 +2271,14 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
         if (lane_id() == 0) stc(&sg[wave_id() * J + j], sj);
       }
     }
-    block_sum2(Sc, nz, L.s);  // its barriers also complete the histogram
-    if (threadIdx.x == 0) {
-      stc(&sl[c].b, Sc);
-      stc(&sl[c].c, (u64)nz);
+    if (p.topp) {
+      lds_sync();  // the histogram is complete (the chunk's sums are not needed: the lists replace them)
+    } else {
+      block_sum2(Sc, nz, L.s);
+      if (threadIdx.x == 0) {
+        stc(&sl[c].b, Sc);
+        stc(&sl[c].c, (u64)nz);
+      }
     }
     QS_TR(6);
     if (p.topp) {
@@ -2313,26 +2317,41 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
         ok = wait_count(a, row, &sy->barB, (u32)a.G * (u32)(r + 1), L.s);
         QS_TR(9 + 4 * r);
         if (!ok) break;
-        // the row's bins: the crossing bin and the mass above it
-        const int b = threadIdx.x;
-        const u64 bm = b < kNB ? ldc(&hr[(size_t)r * kNB + b]) : 0ull;
-        u64 tot;
-        const u64 ex = block_excl64(bm, L.s, &tot);
-        if (r == 0) Tp = mul_frac(tot, p.tp);
-        const u64 target = Tp - A;
-        if (threadIdx.x == 0) L.s.r[12] = 0xffffffffu;
-        lds_sync();
-        if (b < kNB && ex <= target && target < ex + bm) {
-          L.s.r[12] = (u32)b;
-          L.s.r64[12] = ex;
-          // tokens of the bin: at most its mass over its least weight
-          const float wl = bin_least_weight(mb, b, SH);
-          L.s.r[13] = (float)bm <= wl * (float)kFCap ? 1u : 0u;
+        // the row's bins: the crossing bin and the mass above it, by one wave
+        // (bins 4l .. 4l + 3 in lane l), the choice to the others through LDS
+        if (threadIdx.x < 64) {
+          static_assert(kNB == 256, "four bins per lane");
+          const int l = (int)lane_id();
+          u64 bm4[4], sb = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            bm4[i] = ldc(&hr[(size_t)r * kNB + 4 * l + i]);
+            sb += bm4[i];
+          }
+          const u64 inc = wave_incl_scan64(sb);
+          if (r == 0) Tp = mul_frac(readlane64(inc, 63), p.tp);
+          const u64 target = Tp - A;
+          u64 ex = inc - sb;
+          if (l == 0) L.s.r[12] = 0xffffffffu;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (ex <= target && target < ex + bm4[i]) {
+              const int b = 4 * l + i;
+              L.s.r[12] = (u32)b;
+              L.s.r64[12] = ex;
+              // tokens of the bin: at most its mass over its least weight
+              const float wl = bin_least_weight(mb, b, SH);
+              L.s.r[13] = (float)bm4[i] <= wl * (float)kFCap ? 1u : 0u;
+            }
+            ex += bm4[i];
+          }
+          if (l == 0) L.s.r64[13] = Tp;
         }
         lds_sync();
         const u32 bsel = uni(L.s.r[12]);
         const u32 small = uni(L.s.r[13]);
         const u64 exs = uni64(L.s.r64[12]);
+        Tp = uni64(L.s.r64[13]);
         lds_sync();
         if (bsel == 0xffffffffu || (!small && r + 1 == kRounds)) {
           fail_row(a, row, kStList);
