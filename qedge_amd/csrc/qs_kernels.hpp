@@ -2370,8 +2370,9 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
         QS_TR(10 + 4 * r);
       }
       if (ok) {
-        // mass above the bracket (per segment too), and the bracket's tokens listed in id order
-        u64 above = 0;
+        // mass above the bracket (per segment too), and the bracket's tokens listed in
+        // id order; the waves' totals, masses and counts in one exchange
+        u64 above_w = 0;
         u32 cnt[J];
         u64* sg = seg_base(a, row) + (size_t)c * kSegMax;
 #pragma unroll
@@ -2384,22 +2385,26 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
             sj += ((abv >> i) & 1u) ? wunpack(wp[i]) : 0ull;
             cnt[j] += (inb >> i) & 1u;
           }
-          above += sj;
           sj = wave_sum64(sj);
+          above_w += sj;
           if (lane_id() == 0) stc(&sg[wave_id() * J + j], sj);
         }
-        u32 na = (u32)__popc(abv);
-        block_sum2(above, na, L.s);
+        const u32 na_w = wave_sum((u32)__popc(abv));
         u32 ex[J], tot = 0;
+        static_assert(J <= 4, "the exchange holds four vector counts per wave");
 #pragma unroll
         for (int j = 0; j < J; ++j) {
           const u32 inc = wave_incl_scan(cnt[j]);
           ex[j] = inc - cnt[j];
           const u32 tj = readlane(inc, 63);
-          L.s.v[wave_id()][j] = tj;
+          if (lane_id() == 0) L.s.v[wave_id()][j] = tj;
           tot += tj;
         }
-        if (lane_id() == 0) L.s.r[wave_id()] = tot;
+        if (lane_id() == 0) {
+          L.s.r[wave_id()] = tot;
+          L.s.w[wave_id()][0] = above_w;
+          L.s.v[wave_id()][4] = na_w;
+        }
         lds_sync();
         u32 woff = 0, nl = 0;
 #pragma unroll
@@ -2416,7 +2421,15 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
             run += L.s.v[wave_id()][j];
           }
         }
-        lds_sync();
+        u64 above = 0;
+        u32 na = 0;
+        if (threadIdx.x == 0) {
+#pragma unroll
+          for (int i = 0; i < kWaves; ++i) {
+            above += L.s.w[i][0];
+            na += L.s.v[i][4];
+          }
+        }
         u64* lst = list_base(a, row) + (size_t)c * kLC;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
