@@ -1169,6 +1169,27 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
   return r;
 }
 
+// Maxima of two values and the sum of a third over the workgroup, with one
+// pair of barriers.
+__device__ __forceinline__ void block_max2_sum(u32& x, u32& y, u32& z, Scratch& s) {
+  x = wave_max(x);
+  y = wave_max(y);
+  z = wave_sum(z);
+  if (lane_id() == 0) {
+    s.v[wave_id()][5] = x;
+    s.v[wave_id()][6] = y;
+    s.v[wave_id()][7] = z;
+  }
+  lds_sync();
+  x = y = z = 0u;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    x = max(x, s.v[i][5]);
+    y = max(y, s.v[i][6]);
+    z += s.v[i][7];
+  }
+  lds_sync();
+}
 // Maxima of two values over the workgroup with one pair of barriers.
 __device__ __forceinline__ void block_max2(u32& x, u32& y, Scratch& s) {
   x = wave_max(x);
@@ -2587,9 +2608,10 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
           bkmin = key ? max(bkmin, ~key) : bkmin;
         }
       }
-      block_max2(bkmax, bkmin, L.s);
-      nat = block_sum(nat, L.s);
+      block_max2_sum(bkmax, bkmin, nat, L.s);
       bkmin = ~bkmin;
+      // (the per-chunk tie counts are cleared here: the select's barriers order it)
+      for (int cc = threadIdx.x; cc < a.G; cc += kThreads) L.cties[cc] = 0u;
       const SelRes q = held_select<true>(a, L, h, wq, max(bkmin, 1u), bkmax, Tp - Ahi);
       if (!q.ok) {
         fine = false;
@@ -2602,8 +2624,6 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
         W = A + (u64)jties * wt;
         kept = nat + q.cnt_above + jties;
         // per chunk: listed mass above kappa_p and ties at it; the jties-th tie's id
-        for (int cc = threadIdx.x; cc < a.G; cc += kThreads) L.cties[cc] = 0u;
-        lds_sync();
         u32 tcount = 0;
 #pragma unroll
         for (int i = 0; i < kFPer; ++i) {
