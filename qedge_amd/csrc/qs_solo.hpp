@@ -22,6 +22,7 @@ constexpr int kSoloList = 2048;   // bracket tokens listed in LDS
 constexpr int kSoloSegs = 1024;   // segments per row (G * kWaves * J)
 constexpr int kSoloRounds = 6;    // bracket rounds: the first in x = q* - q, then in key space
 constexpr int kSoloHist = 4096;   // history ids copied to LDS (the rest are read from memory)
+constexpr int kSoloCBuf = 128;    // pass 3: tokens at or below the bracket per wave and chunk, compacted
 
 struct SoloFin {
   u64 ent[kSoloList];  // listed tokens (key << 32 | id), in no particular order
@@ -43,6 +44,7 @@ struct SoloLds {
   u32 hc[kNB];           // and tokens per bin (key-space rounds)
   u64 seg[kSoloSegs];    // per segment: total mass, then the mass above the bracket, then kept mass
   u32 segt[kSoloSegs];   // per segment: tokens at the boundary key (a bracket of one key)
+  u64 cbuf[kWaves][kSoloCBuf];  // pass 3: each wave's tokens at or below the bracket, compacted
   u32 nlist;
   Scratch s;
 };
@@ -94,6 +96,17 @@ __device__ __forceinline__ int bracket_side(const Bracket& br, u32 k) {
   return k > br.hi ? 0 : (k < br.lo ? 2 : 1);
 }
 
+#ifdef QS_TRACE
+#define QS_TRS(i)                                                                  \
+  do {                                                                             \
+    if (a.trace && threadIdx.x == 0) a.trace[(size_t)row * a.G * 32 + (i)] = wall_clock64(); \
+  } while (0)
+#else
+#define QS_TRS(i) \
+  do {            \
+  } while (0)
+#endif
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_solo(Args a) {
   __shared__ SoloLds L;
@@ -108,6 +121,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     for (int i = threadIdx.x; i < min(p.hlen, kSoloHist); i += kThreads) L.hist[i] = gld(p.hist + i);
     lds_sync();
   }
+  QS_TRS(0);
   // ---- pass 1: key range of q, or the greedy id
   if (p.kind == kKindGreedy) {
     u64 best = 0;
@@ -188,6 +202,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     return;
   }
   const float qs = f_of_key(kmax);
+  QS_TRS(1);
   // ---- top-k: the k-th largest key (ties kept), by key histograms
   u32 kk = 1u;
   if ((p.kind == kKindTopK || p.kind == kKindSingle) && nnan > (u32)p.k) {
@@ -243,6 +258,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     return x >= pthr ? x : 0u;
   };
   const int nseg = a.G * kWaves * J;
+  QS_TRS(2);
   // ---- pass 2: weights, S, per-segment masses, the first bracket histogram
   Bracket br;
   br.mb0 = mass_bins_first(qs - f_of_key(kmin));
@@ -283,6 +299,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   bool single = false;  // the bracket holds one key (too many tokens to list)
   u32 jties = 0u;
   if (p.topp) {
+    QS_TRS(3);
     // ---- the bracket rounds
     const u64 Tp = mul_frac(S, p.tp);
     bool listed = false;
@@ -394,41 +411,87 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
       return;
     }
+    QS_TRS(4);
     // ---- pass 3: the bracket's tokens listed, the mass above it per segment
     if (threadIdx.x == 0) L.nlist = 0u;
     for (int i = threadIdx.x; i < nseg; i += kThreads) L.segt[i] = 0u;
     lds_sync();
     u32 nzb = 0;  // tokens at or below the bracket with nonzero weight
+    // The weights are needed only for the tokens at or below the bracket (a few
+    // percent for top-p near 1): each wave compacts them through LDS and its
+    // lanes take them in turn, instead of every element position running the
+    // weight for the few lanes that need it.  Above kSoloCBuf of them in a
+    // wave's share of a chunk, the wave takes its elements in place.
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
       with_pen(p.pen, [&](auto pen) {
         constexpr bool PEN = decltype(pen)::value;
+        constexpr int E = kEPT;
         u32 pw[kEPT / 2] = {};
         if constexpr (PEN) chunk_counts(L, ch, c, pw);
+        u32 ks[E];
+        u32 fl = 0;  // bit i: element i lies at or below the bracket
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          u64 sub = 0;
-          u32 ties = 0;
+        for (int j = 0; j < J; ++j)
 #pragma unroll
           for (int e = 0; e < VL; ++e) {
-            const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-            const u32 k = skey(q);
-            if (!k) continue;
-            const int side = bracket_side(br, k);
-            if (side == 0) continue;
-            const u64 w = wunpack(wpk(q, k));
-            sub += w;
-            nzb += w ? 1u : 0u;
-            if (side == 1 && w) {
-              if (single) {
-                ++ties;
-              } else {
-                const u32 slot = atomicAdd(&L.nlist, 1u);
-                if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)ch.id(j, e);
-              }
+            const int i = j * VL + e;
+            ks[i] = skey(qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one));
+            fl |= (ks[i] != 0u && ks[i] <= br.hi) ? 1u << i : 0u;
+          }
+        const u32 cnt = (u32)__popc(fl);
+        const u32 incl = wave_incl_scan(cnt);
+        const u32 total = readlane(incl, 63);
+        u64 subj[J];
+        u32 tiesj[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          subj[j] = 0;
+          tiesj[j] = 0;
+        }
+        // one token at or below the bracket: its weight to its vector's sum, the
+        // bracket's tokens listed (or counted, for a bracket of one key)
+        auto take = [&](u32 k, int j, int e, u32 lane) {
+          const int side = bracket_side(br, k);
+          const u64 w = wunpack(wpk(f_of_key(k), k));
+#pragma unroll
+          for (int jj = 0; jj < J; ++jj) subj[jj] += jj == j ? w : 0ull;
+          nzb += w ? 1u : 0u;
+          if (side == 1 && w) {
+            if (single) {
+#pragma unroll
+              for (int jj = 0; jj < J; ++jj) tiesj[jj] += jj == j ? 1u : 0u;
+            } else {
+              const u32 slot = atomicAdd(&L.nlist, 1u);
+              const int id = c * kCH + wave_id() * kWaveSpan + (int)lane * VL + j * 64 * VL + e;
+              if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)id;
             }
           }
-          const u64 sw = wave_sum64(sub);
-          const u32 tw = wave_sum(ties);
+        };
+        if (total <= (u32)kSoloCBuf) {
+          u64* cb = L.cbuf[wave_id()];
+          u32 pos = incl - cnt;
+#pragma unroll
+          for (int i = 0; i < E; ++i)
+            if ((fl >> i) & 1u) cb[pos++] = ((u64)ks[i] << 32) | (lane_id() << 4) | (u32)i;
+          // the wave's own LDS writes: complete before its lanes read each other's
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          for (u32 x = lane_id(); x < total; x += 64) {
+            const u64 en = cb[x];
+            const u32 i = (u32)en & 15u;
+            take((u32)(en >> 32), (int)(i / VL), (int)(i % VL), ((u32)en >> 4) & 63u);
+          }
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // read before the next chunk writes the buffer again
+        } else {
+#pragma unroll
+          for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int e = 0; e < VL; ++e)
+              if ((fl >> (j * VL + e)) & 1u) take(ks[j * VL + e], j, e, lane_id());
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const u64 sw = wave_sum64(subj[j]);
+          const u32 tw = wave_sum(tiesj[j]);
           if (lane_id() == 0) {
             const int sg = (c * kWaves + wave_id()) * J + j;
             L.seg[sg] -= sw;
@@ -553,6 +616,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       lds_sync();
     }
   }
+  QS_TRS(5);
   // ---- the draw: the segment holding t, then the token inside it
   const u64 t = mul_frac(W, p.u);
   {
@@ -594,6 +658,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   const u32 pick = L.s.r[15];
   write_result(a, row, p, pick == 0xffffffffu ? -1ll : (long long)pick, W, thr, kPathSolo,
                pick == 0xffffffffu ? kStIncomplete : 0u, kmax, klo, idlo, kept);
+  QS_TRS(6);
 }
 
 }  // namespace qs
