@@ -390,6 +390,22 @@ __device__ __forceinline__ u64 wunpack(u32 wp) {
   const int s = (int)(wp >> 24) - 64;
   return (m << (s > 0 ? s : 0)) >> (s < 0 ? min(-s, 63) : 0);
 }
+// The same weight as wunpack(wpack_of(q, skey(q), qs, skey(qs), SH)) for a
+// finite row maximum qs, from d = q - qs and without the key: d is 0 at the
+// maximum (also for -0 against +0), NaN for a NaN q and -inf for q = -inf.
+// flmin = -(SH + 40) clamps the shift to s >= -40, where the weights below 1
+// (s <= -24, which takes in the NaN and -inf tokens) come out of the right
+// shift as 0 since m < 2^24; every weight of 1 or more has its s unchanged.
+__device__ __forceinline__ u64 weight_finite(float d, float flmin, int SH) {
+  const float y = d * kL2E;
+  const float fl = __builtin_floorf(y);
+  const float f = y - fl;
+  float p = exp2_poly(f);
+  p = __builtin_amdgcn_fmed3f(p, 1.0f, __uint_as_float(0x3fffffffu));
+  const u64 m = 0x800000u | (__float_as_uint(p) & 0x7fffffu);
+  const int s = (int)fmaxf(fl, flmin) + SH;
+  return (m << max(s, 0)) >> max(-s, 0);
+}
 __device__ __forceinline__ u64 weight_of(float q, u32 k, float qs, u32 ks, int SH) {
   return wunpack(wpack_of(q, k, qs, ks, SH));
 }

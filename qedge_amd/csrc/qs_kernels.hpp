@@ -355,6 +355,10 @@ __device__ __forceinline__ void with_pen(bool pen, F&& f) {
   else
     f(Tag<false>{});
 }
+template <int M>
+struct ITag {
+  static constexpr int value = M;
+};
 // elem_zc with the penalty flag known at compile time.
 template <bool PEN, int DT>
 __device__ __forceinline__ float elem_zt(const Chunk<DT>& ch, const RowP& p, const u32 (&pw)[kEPT / 2], int j, int e) {
@@ -1587,11 +1591,13 @@ __device__ __forceinline__ MassBins mass_bins_first(float D) {
 }
 // The two segments make a concave map (s1 >= s2: 16 bins per unit, then at most
 // 64 / 4), so the bin position is the smaller of the two lines.
-__device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, const MassBins& m) {
-  const float d = (k == ks) ? 0.0f : q - qs;
+__device__ __forceinline__ u32 mass_bin_d(float d, const MassBins& m) {
   const float x = -d - m.x0;
   const float f = fminf(x * m.s1, __builtin_fmaf(x, m.s2, m.c2));
   return min((u32)kNB - 1u, (u32)fmaxf(0.0f, f));
+}
+__device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, const MassBins& m) {
+  return mass_bin_d((k == ks) ? 0.0f : q - qs, m);
 }
 // x at the far edge of bin b
 __device__ __forceinline__ float bin_edge(const MassBins& m, u32 b) {

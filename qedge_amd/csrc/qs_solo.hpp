@@ -269,28 +269,53 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   lds_sync();
   u64 S = 0;
   u32 nz = 0;
+  // With a finite maximum (every row with a finite q) the weights come from
+  // d = q - qs without keys; mode 1 also drops the division (T = 1) and the
+  // top-k and min-p tests (none set).  Mode 0 is the keyed form for a row
+  // whose maximum is +inf or -inf.
+  const int wmode = !(qs - qs == 0.0f) ? 0 : ((p.t_one && kk == 1u && thr == 0ull) ? 1 : 2);
+  const float flmin = -(float)(SH + 40);
+  const float qk = kk > 1u ? f_of_key(kk) : -__builtin_inff();  // q >= qk: key >= kk
   solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
     with_pen(p.pen, [&](auto pen) {
       constexpr bool PEN = decltype(pen)::value;
       u32 pw[kEPT / 2] = {};
       if constexpr (PEN) chunk_counts(L, ch, c, pw);
+      auto body = [&](auto mode) {
+        constexpr int M = decltype(mode)::value;
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        u64 sj = 0;
+        for (int j = 0; j < J; ++j) {
+          u64 sj = 0;
 #pragma unroll
-        for (int e = 0; e < VL; ++e) {
-          const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-          const u32 k = skey(q);
-          const u32 x = wpk(q, k);
-          const u64 w = wunpack(x);
-          sj += w;
-          nz += x ? 1u : 0u;
-          if (p.topp && x) atomicAdd(&L.mh[mass_bin(q, k, qs, kmax, br.mb0)], w);
+          for (int e = 0; e < VL; ++e) {
+            const float z = elem_zt<PEN>(ch, p, pw, j, e);
+            u64 w;
+            if constexpr (M == 0) {
+              const float q = qdiv(z, p.T, p.rT, p.t_one);
+              const u32 k = skey(q);
+              w = wunpack(wpk(q, k));
+              if (p.topp && w) atomicAdd(&L.mh[mass_bin(q, k, qs, kmax, br.mb0)], w);
+            } else {
+              const float q = M == 1 ? z : qdiv(z, p.T, p.rT, p.t_one);
+              const float d = q - qs;
+              w = weight_finite(d, flmin, SH);
+              if constexpr (M == 2) w = (q >= qk && w >= thr) ? w : 0ull;
+              if (p.topp && w) atomicAdd(&L.mh[mass_bin_d(d, br.mb0)], w);
+            }
+            sj += w;
+            nz += w ? 1u : 0u;
+          }
+          const u64 sw = wave_sum64(sj);
+          if (lane_id() == 0) L.seg[(c * kWaves + wave_id()) * J + j] = sw;
+          S += lane_id() == 0 ? sw : 0ull;
         }
-        const u64 sw = wave_sum64(sj);
-        if (lane_id() == 0) L.seg[(c * kWaves + wave_id()) * J + j] = sw;
-        S += lane_id() == 0 ? sw : 0ull;
-      }
+      };
+      if (wmode == 1)
+        body(ITag<1>{});
+      else if (wmode == 2)
+        body(ITag<2>{});
+      else
+        body(ITag<0>{});
     });
   });
   block_sum2(S, nz, L.s);

@@ -72,6 +72,10 @@ def test_rare_branches(gpu, dtype):
     y = (x * 0.05).astype(np.float32); y[rng.integers(V, size=50)] = np.inf
     rows.append(y); T.append(1.0); P.append(0.9); K.append(0); MP.append(0.0)            # +inf tokens
     z = np.round(x * 4) / 4; rows.append(z.astype(np.float32)); T.append(1.0); P.append(0.7); K.append(0); MP.append(0.0)
+    v = (x * 0.5).astype(np.float32); v[rng.integers(V, size=300)] = -np.inf; v[rng.integers(V, size=300)] = np.nan
+    rows.append(v); T.append(1.0); P.append(0.9); K.append(0); MP.append(0.0)           # -inf and NaN among finite
+    n = np.full(V, -np.inf, np.float32); n[rng.integers(V, size=40)] = np.nan
+    rows.append(n); T.append(1.0); P.append(0.5); K.append(0); MP.append(0.0)           # maximum -inf
     X = np.stack(rows)
     if dtype == "bf16":
         X = _bf16(X)
