@@ -447,48 +447,46 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     // lanes take them in turn, instead of every element position running the
     // weight for the few lanes that need it.  Above kSoloCBuf of them in a
     // wave's share of a chunk, the wave takes its elements in place.
+    // key <= br.hi as q <= qhi (NaN fails both); no token has the key
+    // 0x7fffffff (skey folds -0 into +0), whose q would be -0 and admit +0
+    const float qhi = f_of_key(br.hi == 0x7fffffffu ? 0x7ffffffeu : br.hi);
     solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
       with_pen(p.pen, [&](auto pen) {
         constexpr bool PEN = decltype(pen)::value;
         constexpr int E = kEPT;
         u32 pw[kEPT / 2] = {};
         if constexpr (PEN) chunk_counts(L, ch, c, pw);
-        u32 ks[E];
+        float qv[E];
         u32 fl = 0;  // bit i: element i lies at or below the bracket
 #pragma unroll
         for (int j = 0; j < J; ++j)
 #pragma unroll
           for (int e = 0; e < VL; ++e) {
             const int i = j * VL + e;
-            ks[i] = skey(qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one));
-            fl |= (ks[i] != 0u && ks[i] <= br.hi) ? 1u << i : 0u;
+            qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+            fl |= qv[i] <= qhi ? 1u << i : 0u;
           }
         const u32 cnt = (u32)__popc(fl);
         const u32 incl = wave_incl_scan(cnt);
         const u32 total = readlane(incl, 63);
-        u64 subj[J];
-        u32 tiesj[J];
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-          subj[j] = 0;
-          tiesj[j] = 0;
-        }
-        // one token at or below the bracket: its weight to its vector's sum, the
-        // bracket's tokens listed (or counted, for a bracket of one key)
-        auto take = [&](u32 k, int j, int e, u32 lane) {
+        const int sg0 = (c * kWaves + wave_id()) * J;
+        // one token at or below the bracket: its weight off its segment's mass,
+        // the bracket's tokens listed (or counted, for a bracket of one key)
+        auto take = [&](float q, int j, int e, u32 lane) {
+          const u32 k = skey(q);
           const int side = bracket_side(br, k);
-          const u64 w = wunpack(wpk(f_of_key(k), k));
-#pragma unroll
-          for (int jj = 0; jj < J; ++jj) subj[jj] += jj == j ? w : 0ull;
-          nzb += w ? 1u : 0u;
-          if (side == 1 && w) {
-            if (single) {
-#pragma unroll
-              for (int jj = 0; jj < J; ++jj) tiesj[jj] += jj == j ? 1u : 0u;
-            } else {
-              const u32 slot = atomicAdd(&L.nlist, 1u);
-              const int id = c * kCH + wave_id() * kWaveSpan + (int)lane * VL + j * 64 * VL + e;
-              if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)id;
+          const u64 w = wunpack(wpk(q, k));
+          if (w) {
+            atomicAdd(&L.seg[sg0 + j], (u64)0 - w);
+            ++nzb;
+            if (side == 1) {
+              if (single) {
+                atomicAdd(&L.segt[sg0 + j], 1u);
+              } else {
+                const u32 slot = atomicAdd(&L.nlist, 1u);
+                const int id = c * kCH + wave_id() * kWaveSpan + (int)lane * VL + j * 64 * VL + e;
+                if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)id;
+              }
             }
           }
         };
@@ -497,13 +495,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
           u32 pos = incl - cnt;
 #pragma unroll
           for (int i = 0; i < E; ++i)
-            if ((fl >> i) & 1u) cb[pos++] = ((u64)ks[i] << 32) | (lane_id() << 4) | (u32)i;
+            if ((fl >> i) & 1u) cb[pos++] = ((u64)__float_as_uint(qv[i]) << 32) | (lane_id() << 4) | (u32)i;
           // the wave's own LDS writes: complete before its lanes read each other's
           __builtin_amdgcn_s_waitcnt(0xC07F);
           for (u32 x = lane_id(); x < total; x += 64) {
             const u64 en = cb[x];
             const u32 i = (u32)en & 15u;
-            take((u32)(en >> 32), (int)(i / VL), (int)(i % VL), ((u32)en >> 4) & 63u);
+            take(__uint_as_float((u32)(en >> 32)), (int)(i / VL), (int)(i % VL), ((u32)en >> 4) & 63u);
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);  // read before the next chunk writes the buffer again
         } else {
@@ -511,17 +509,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
           for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int e = 0; e < VL; ++e)
-              if ((fl >> (j * VL + e)) & 1u) take(ks[j * VL + e], j, e, lane_id());
-        }
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-          const u64 sw = wave_sum64(subj[j]);
-          const u32 tw = wave_sum(tiesj[j]);
-          if (lane_id() == 0) {
-            const int sg = (c * kWaves + wave_id()) * J + j;
-            L.seg[sg] -= sw;
-            L.segt[sg] = tw;
-          }
+              if ((fl >> (j * VL + e)) & 1u) take(qv[j * VL + e], j, e, lane_id());
         }
       });
     });
