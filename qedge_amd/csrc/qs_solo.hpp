@@ -61,22 +61,94 @@ __device__ __forceinline__ int seg_of(int id) {
   return id / (64 * Chunk<DT>::VL);
 }
 
+// Loads of chunk c for the streaming passes with 16-byte vectors (Args::vec_ok
+// and V >= VL): one vector load each, always issued, so that the number of
+// loads in flight does not depend on the data and the next chunk's loads stay
+// in flight while this one is worked on.  A vector that is not wholly below V
+// reads the row's first vector instead; chunk_tail completes the chunk holding
+// V before use.
+template <int DT>
+__device__ __forceinline__ void load_chunk_vec(const Args& a, int row, int c, Chunk<DT>& ch) {
+  constexpr int VL = Chunk<DT>::VL;
+  ch.base = c * kCH + wave_id() * kWaveSpan + lane_id() * VL;
+  ch.nval = a.V - ch.base;
+  const char* rp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * (16 / VL);
+#pragma unroll
+  for (int j = 0; j < Chunk<DT>::J; ++j) {
+    const int i0 = ch.base + j * 64 * VL;
+    const int at = i0 + VL <= a.V ? i0 : 0;
+    ch.v[j] = gld((const uint4*)(rp + (size_t)at * (16 / VL)));
+  }
+}
+// The vector holding id V - 1 when V is not a multiple of VL: its ids below V,
+// NaN past them (NaN padding everywhere when V is a multiple of VL).
+template <int DT>
+__device__ __forceinline__ uint4 row_tail_vec(const Args& a, int row) {
+  constexpr int VL = Chunk<DT>::VL;
+  const int i0 = a.V / VL * VL;
+  const u32 pad = DT == QS_DTYPE_F32 ? 0x7fc00000u : 0x7fc07fc0u;
+  u32 x[4] = {pad, pad, pad, pad};
+  const size_t rowoff = (size_t)row * (size_t)a.row_stride;
+  if (DT == QS_DTYPE_F32) {
+    const float* q = (const float*)a.logits + rowoff;
+    for (int e = 0; e < 4; ++e)
+      if (i0 + e < a.V) x[e] = __float_as_uint(gld(q + i0 + e));
+  } else {
+    const uint16_t* q = (const uint16_t*)a.logits + rowoff;
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e < a.V) x[e >> 1] = (x[e >> 1] & ~(0xffffu << ((e & 1) * 16))) | ((u32)gld(q + i0 + e) << ((e & 1) * 16));
+  }
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+// The chunk holding V: the vector across V from tv, NaN past it.
+template <int DT>
+__device__ __forceinline__ void chunk_tail(const Args& a, Chunk<DT>& ch, const uint4& tv) {
+  constexpr int VL = Chunk<DT>::VL;
+  const u32 pad = DT == QS_DTYPE_F32 ? 0x7fc00000u : 0x7fc07fc0u;
+#pragma unroll
+  for (int j = 0; j < Chunk<DT>::J; ++j) {
+    const int i0 = ch.base + j * 64 * VL;
+    if (i0 + VL > a.V) ch.v[j] = i0 < a.V ? tv : make_uint4(pad, pad, pad, pad);
+  }
+}
+
 // f(ch, c) over the row's chunks, with chunk c + 1's loads in flight during
-// chunk c and the history table built per chunk.
-template <int DT, typename F>
-__device__ __forceinline__ void solo_pass(const Args& a, const RowP& p, int row, SoloLds& L, F&& f) {
+// chunk c and the history table built per chunk.  VEC: the loads of
+// load_chunk_vec (the chunk past the last re-reads the last chunk, which is
+// never worked on), tv the row's tail vector.
+template <int DT, bool VEC, typename F>
+__device__ __forceinline__ void solo_pass(const Args& a, const RowP& p, int row, SoloLds& L, const uint4& tv, F&& f) {
   Chunk<DT> b0, b1;
-  load_chunk<DT>(a, row, 0, b0);
-  for (int c = 0; c < a.G; c += 2) {
-    if (c + 1 < a.G) load_chunk<DT>(a, row, c + 1, b1);
-    if (p.pen) pen_build(p, c, L);
-    f(b0, c);
-    if (p.pen) lds_sync();
-    if (c + 1 >= a.G) break;
-    if (c + 2 < a.G) load_chunk<DT>(a, row, c + 2, b0);
-    if (p.pen) pen_build(p, c + 1, L);
-    f(b1, c + 1);
-    if (p.pen) lds_sync();
+  if constexpr (VEC) {
+    const int last = a.G - 1;
+    const bool tail = a.V % kCH != 0;  // the last chunk holds V
+    load_chunk_vec<DT>(a, row, 0, b0);
+    for (int c = 0; c < a.G; c += 2) {
+      load_chunk_vec<DT>(a, row, min(c + 1, last), b1);
+      if (p.pen) pen_build(p, c, L);
+      if (tail && c == last) chunk_tail<DT>(a, b0, tv);
+      f(b0, c);
+      if (p.pen) lds_sync();
+      if (c + 1 >= a.G) break;
+      load_chunk_vec<DT>(a, row, min(c + 2, last), b0);
+      if (p.pen) pen_build(p, c + 1, L);
+      if (tail && c + 1 == last) chunk_tail<DT>(a, b1, tv);
+      f(b1, c + 1);
+      if (p.pen) lds_sync();
+    }
+  } else {
+    load_chunk<DT>(a, row, 0, b0);
+    for (int c = 0; c < a.G; c += 2) {
+      if (c + 1 < a.G) load_chunk<DT>(a, row, c + 1, b1);
+      if (p.pen) pen_build(p, c, L);
+      f(b0, c);
+      if (p.pen) lds_sync();
+      if (c + 1 >= a.G) break;
+      if (c + 2 < a.G) load_chunk<DT>(a, row, c + 2, b0);
+      if (p.pen) pen_build(p, c + 1, L);
+      f(b1, c + 1);
+      if (p.pen) lds_sync();
+    }
   }
 }
 
@@ -107,13 +179,15 @@ __device__ __forceinline__ int bracket_side(const Bracket& br, u32 k) {
   } while (0)
 #endif
 
-template <int DT>
+// VEC: the logits in 16-byte vectors (Args::vec_ok) and V >= VL.
+template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_solo(Args a) {
   __shared__ SoloLds L;
   constexpr int J = Chunk<DT>::J, VL = Chunk<DT>::VL;
   const int row = (int)uni(a.order ? (u32)gld(a.order + blockIdx.x) : blockIdx.x);
   if ((unsigned)row >= (unsigned)a.B) return;
   const RowP p = row_params(a, row);
+  const uint4 tv = VEC ? row_tail_vec<DT>(a, row) : make_uint4(0u, 0u, 0u, 0u);
   const int SH = a.SH;
   const u64 thr = ceil_scaled(p.mp, 23 + SH);
   const u32 pthr = uni(packed_threshold(thr));
@@ -125,7 +199,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   // ---- pass 1: key range of q, or the greedy id
   if (p.kind == kKindGreedy) {
     u64 best = 0;
-    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+    solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
       with_pen(p.pen, [&](auto pen) {
         constexpr bool PEN = decltype(pen)::value;
         u32 pw[kEPT / 2] = {};
@@ -151,7 +225,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     // z is the logit: q* and q_min are the quotients of its maximum and minimum
     // (z / T is monotone), which NaN-ignoring max / min find; NaN past V
     float zmx = -__builtin_inff(), zmn = __builtin_inff();
-    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+    solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
       (void)c;
 #pragma unroll
       for (int j = 0; j < J; ++j)
@@ -172,7 +246,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     }
     gbest = 0xffffffffu;  // every z NaN: the first id
   } else {
-    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+    solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
       with_pen(p.pen, [&](auto pen) {
         constexpr bool PEN = decltype(pen)::value;
         u32 pw[kEPT / 2] = {};
@@ -213,7 +287,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       lds_sync();
       const int bl = bitlen(hi - lo);
       const int sh = bl > 8 ? bl - 8 : 0;
-      solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+      solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
         with_pen(p.pen, [&](auto pen) {
           constexpr bool PEN = decltype(pen)::value;
           u32 pw[kEPT / 2] = {};
@@ -276,7 +350,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   const int wmode = !(qs - qs == 0.0f) ? 0 : ((p.t_one && kk == 1u && thr == 0ull) ? 1 : 2);
   const float flmin = -(float)(SH + 40);
   const float qk = kk > 1u ? f_of_key(kk) : -__builtin_inff();  // q >= qk: key >= kk
-  solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+  solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
     with_pen(p.pen, [&](auto pen) {
       constexpr bool PEN = decltype(pen)::value;
       u32 pw[kEPT / 2] = {};
@@ -339,7 +413,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         const u32 lo = rlo, hi = rhi;
         const int bl = bitlen(hi - lo);
         const int sh = bl > 8 ? bl - 8 : 0;
-        solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+        solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
           with_pen(p.pen, [&](auto pen) {
             constexpr bool PEN = decltype(pen)::value;
             u32 pw[kEPT / 2] = {};
@@ -450,7 +524,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     // key <= br.hi as q <= qhi (NaN fails both); no token has the key
     // 0x7fffffff (skey folds -0 into +0), whose q would be -0 and admit +0
     const float qhi = f_of_key(br.hi == 0x7fffffffu ? 0x7ffffffeu : br.hi);
-    solo_pass<DT>(a, p, row, L, [&](const Chunk<DT>& ch, int c) {
+    solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
       with_pen(p.pen, [&](auto pen) {
         constexpr bool PEN = decltype(pen)::value;
         constexpr int E = kEPT;

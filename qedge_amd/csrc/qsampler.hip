@@ -192,10 +192,19 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   const int J = logits_dtype == QS_DTYPE_F32 ? 4 : 2;  // 16-byte vectors per thread and chunk
   const bool solo = (flags & QS_FLAG_SOLO) && L.G * kWaves * J <= kSoloSegs;
   if (solo) {
-    if (logits_dtype == QS_DTYPE_F32)
-      hipLaunchKernelGGL(k_solo<QS_DTYPE_F32>, dim3(B), block, 0, stream, a);
-    else
-      hipLaunchKernelGGL(k_solo<QS_DTYPE_BF16>, dim3(B), block, 0, stream, a);
+    // 16-byte vector loads need aligned rows and at least one whole vector
+    const bool vec = a.vec_ok && a.V >= (logits_dtype == QS_DTYPE_F32 ? 4 : 8);
+    if (logits_dtype == QS_DTYPE_F32) {
+      if (vec)
+        hipLaunchKernelGGL((k_solo<QS_DTYPE_F32, true>), dim3(B), block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((k_solo<QS_DTYPE_F32, false>), dim3(B), block, 0, stream, a);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((k_solo<QS_DTYPE_BF16, true>), dim3(B), block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((k_solo<QS_DTYPE_BF16, false>), dim3(B), block, 0, stream, a);
+    }
   } else if (logits_dtype == QS_DTYPE_F32) {
     hipLaunchKernelGGL(k_sample<QS_DTYPE_F32>, grid, block, 0, stream, a);
   } else {

@@ -21,11 +21,19 @@ def _bf16(x):
 
 
 def _solo(logits, dtype, device, T, P=None, K=None, rep=None, pres=None, freq=None, hist=None, u=None,
-          min_p=None, use_top_p=True):
+          min_p=None, use_top_p=True, pad_to=None):
     B, V = logits.shape
     t = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)
-    lg = (t(logits, torch.float32) if dtype == "f32"
-          else torch.from_numpy(np.ascontiguousarray(logits).view(np.int16)).to(device).view(torch.bfloat16))
+    if pad_to is not None:
+        # rows pad_to apart (16-byte aligned), the columns past V holding +inf,
+        # which no call may read
+        wide = np.full((B, pad_to), np.inf, np.float32) if dtype == "f32" else np.full((B, pad_to), 0x7F80, np.uint16)
+        wide[:, :V] = logits
+    src = logits if pad_to is None else wide
+    lg = (t(src, torch.float32) if dtype == "f32"
+          else torch.from_numpy(np.ascontiguousarray(src).view(np.int16)).to(device).view(torch.bfloat16))
+    if pad_to is not None:
+        lg = lg[:, :V]
     H = 0 if hist is None else hist.shape[1]
     ws = Workspace(B, V, lg.dtype, H, device)
     ids = torch.empty(B, dtype=torch.int64, device=device)
@@ -85,6 +93,25 @@ def test_rare_branches(gpu, dtype):
           min_p=np.array(MP, np.float32))
     # without top-p
     _solo(X, dtype, gpu, np.array(T, np.float32), None, np.array(K, np.int32), u=U, use_top_p=False)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("V", [40961, 3 * 8192 + 5, 16387])
+def test_strided_rows_with_a_vector_across_v(gpu, dtype, V):
+    """Rows 16-byte aligned with V not a multiple of the vector: the vector
+    holding id V - 1 is read by elements, nothing past V is read."""
+    rng = np.random.default_rng(V)
+    B = 6
+    X = (rng.standard_normal((B, V)) * np.array([[0.05], [1.0], [3.0], [2.0], [1.0], [0.5]])).astype(np.float32)
+    X[1, V - 1] = 9.0  # the last id is the largest of row 1
+    if dtype == "bf16":
+        X = _bf16(X)
+    T = np.array([1.0, 0.8, 1.0, 0.0, 1.3, 1.0], np.float32)
+    P = np.array([0.95, 0.9, 0.5, 1.0, 0.99, 1.0], np.float32)
+    K = np.array([0, 0, 0, 0, 50, 0], np.int32)
+    MP = np.array([0.0, 0.0, 0.0, 0.0, 0.0, 0.01], np.float32)
+    pad = (V + 15) // 16 * 16 + 16
+    _solo(X, dtype, gpu, T, P, K, u=rng.random(B).astype(np.float32), min_p=MP, pad_to=pad)
 
 
 def test_penalties_and_long_histories(gpu):
