@@ -98,7 +98,7 @@ __device__ __forceinline__ uint4 row_tail_vec(const Args& a, int row) {
     for (int e = 0; e < 8; ++e)
       if (i0 + e < a.V) x[e >> 1] = (x[e >> 1] & ~(0xffffu << ((e & 1) * 16))) | ((u32)gld(q + i0 + e) << ((e & 1) * 16));
   }
-  return make_uint4(x[0], x[1], x[2], x[3]);
+  return make_uint4(uni(x[0]), uni(x[1]), uni(x[2]), uni(x[3]));  // the same in every lane
 }
 // The chunk holding V: the vector across V from tv, NaN past it.
 template <int DT>
@@ -271,6 +271,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     gbest = block_max64(gbest, L.s);
     nnan = block_sum(nnan, L.s);  // tokens whose q is not NaN
   }
+  // the row's figures are the same in every lane: scalar registers
+  kmax = uni(kmax);
+  kmin = uni(kmin);
+  nnan = uni(nnan);
+  gbest = uni64(gbest);
   if (kmax == 0u) {  // every q is NaN: no weights, the greedy id (as the exact path)
     write_result(a, row, p, (long long)(0xffffffffu - (u32)gbest), 0, thr, kPathSolo, 0u, 0u, 0u, 0u, 0u);
     return;
@@ -393,6 +398,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     });
   });
   block_sum2(S, nz, L.s);
+  S = uni64(S);
+  nz = uni(nz);
   u64 W = S, A = 0, wt = 0;
   u32 klo = kk, idlo = (u32)a.V, kept = nz;  // without top-p: K, the tokens with key >= kk
   bool single = false;  // the bracket holds one key (too many tokens to list)
@@ -515,15 +522,22 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     if (threadIdx.x == 0) L.nlist = 0u;
     for (int i = threadIdx.x; i < nseg; i += kThreads) L.segt[i] = 0u;
     lds_sync();
-    u32 nzb = 0;  // tokens at or below the bracket with nonzero weight
-    // The weights are needed only for the tokens at or below the bracket (a few
-    // percent for top-p near 1): each wave compacts them through LDS and its
-    // lanes take them in turn, instead of every element position running the
-    // weight for the few lanes that need it.  Above kSoloCBuf of them in a
-    // wave's share of a chunk, the wave takes its elements in place.
-    // key <= br.hi as q <= qhi (NaN fails both); no token has the key
-    // 0x7fffffff (skey folds -0 into +0), whose q would be -0 and admit +0
+    // Each segment's mass above the bracket, and the bracket's tokens listed.
+    // Each wave weighs one side per chunk: the tokens at or below the bracket
+    // (their mass off the segment's total) or those above it and in it (the
+    // mass above directly), the side that was the smaller in its previous
+    // chunk, starting with the tokens at or below.  The weighed tokens
+    // are compacted through LDS so that the lanes take them in turn, unless
+    // there are more than kSoloCBuf of them, when the wave takes its elements
+    // in place.
+    u32 nab = 0;      // tokens at or below the bracket (not NaN)
+    bool up = false;  // the wave weighs the tokens above the bracket
+    // key <= br.hi as q <= qhi and key >= br.lo as q >= qlo (NaN fails every
+    // test); no token has the key 0x7fffffff (skey folds -0 into +0), whose q
+    // would be -0 and admit +0, and every key up to that of -inf (0x007fffff)
+    // admits all but NaN
     const float qhi = f_of_key(br.hi == 0x7fffffffu ? 0x7ffffffeu : br.hi);
+    const float qlo = br.lo <= 0x007fffffu ? -__builtin_inff() : f_of_key(br.lo);
     solo_pass<DT, VEC>(a, p, row, L, tv, [&](const Chunk<DT>& ch, int c) {
       with_pen(p.pen, [&](auto pen) {
         constexpr bool PEN = decltype(pen)::value;
@@ -531,64 +545,93 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         u32 pw[kEPT / 2] = {};
         if constexpr (PEN) chunk_counts(L, ch, c, pw);
         float qv[E];
-        u32 fl = 0;  // bit i: element i lies at or below the bracket
+        u32 set = 0;  // bit i: element i above or in the bracket (up), else at or below it
+        if (up) {
+          u32 nv = 0;  // not NaN
 #pragma unroll
-        for (int j = 0; j < J; ++j)
+          for (int j = 0; j < J; ++j)
 #pragma unroll
-          for (int e = 0; e < VL; ++e) {
-            const int i = j * VL + e;
-            qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
-            fl |= qv[i] <= qhi ? 1u << i : 0u;
-          }
-        const u32 cnt = (u32)__popc(fl);
-        const u32 incl = wave_incl_scan(cnt);
-        const u32 total = readlane(incl, 63);
-        const int sg0 = (c * kWaves + wave_id()) * J;
-        // one token at or below the bracket: its weight off its segment's mass,
-        // the bracket's tokens listed (or counted, for a bracket of one key)
-        auto take = [&](float q, int j, int e, u32 lane) {
-          const u32 k = skey(q);
-          const int side = bracket_side(br, k);
-          const u64 w = wunpack(wpk(q, k));
-          if (w) {
-            atomicAdd(&L.seg[sg0 + j], (u64)0 - w);
-            ++nzb;
-            if (side == 1) {
-              if (single) {
-                atomicAdd(&L.segt[sg0 + j], 1u);
-              } else {
-                const u32 slot = atomicAdd(&L.nlist, 1u);
-                const int id = c * kCH + wave_id() * kWaveSpan + (int)lane * VL + j * 64 * VL + e;
-                if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)id;
-              }
+            for (int e = 0; e < VL; ++e) {
+              const int i = j * VL + e;
+              qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+              set |= qv[i] >= qlo ? 1u << i : 0u;
+              nv += qv[i] == qv[i] ? 1u : 0u;
             }
-          }
-        };
-        if (total <= (u32)kSoloCBuf) {
-          u64* cb = L.cbuf[wave_id()];
-          u32 pos = incl - cnt;
-#pragma unroll
-          for (int i = 0; i < E; ++i)
-            if ((fl >> i) & 1u) cb[pos++] = ((u64)__float_as_uint(qv[i]) << 32) | (lane_id() << 4) | (u32)i;
-          // the wave's own LDS writes: complete before its lanes read each other's
-          __builtin_amdgcn_s_waitcnt(0xC07F);
-          for (u32 x = lane_id(); x < total; x += 64) {
-            const u64 en = cb[x];
-            const u32 i = (u32)en & 15u;
-            take(__uint_as_float((u32)(en >> 32)), (int)(i / VL), (int)(i % VL), ((u32)en >> 4) & 63u);
-          }
-          __builtin_amdgcn_s_waitcnt(0xC07F);  // read before the next chunk writes the buffer again
+          nab += nv - (u32)__popc(set);  // below (the bracket's tokens are counted as taken)
         } else {
 #pragma unroll
           for (int j = 0; j < J; ++j)
 #pragma unroll
-            for (int e = 0; e < VL; ++e)
-              if ((fl >> (j * VL + e)) & 1u) take(qv[j * VL + e], j, e, lane_id());
+            for (int e = 0; e < VL; ++e) {
+              const int i = j * VL + e;
+              qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+              set |= qv[i] <= qhi ? 1u << i : 0u;
+            }
+          nab += (u32)__popc(set);
         }
+        const u32 cnt = (u32)__popc(set);
+        const u32 incl = wave_incl_scan(cnt);
+        const u32 total = readlane(incl, 63);
+        const int sg0 = (c * kWaves + wave_id()) * J;
+        // one weighed token: its weight to (above) or off (at or below) its
+        // segment's mass, and a bracket token listed (or counted, for a bracket
+        // of one key); add(j, w) and tie(j) take the segment's share
+        auto take = [&](float q, int j, int e, u32 lane, auto&& add, auto&& tie) {
+          const u32 k = skey(q);
+          const int side = bracket_side(br, k);
+          const u64 w = wunpack(wpk(q, k));
+          if (up ? side == 0 : true) add(j, w);
+          if (up && side == 1) ++nab;
+          if (side == 1 && w) {
+            if (single) {
+              tie(j);
+            } else {
+              const u32 slot = atomicAdd(&L.nlist, 1u);
+              const int id = c * kCH + wave_id() * kWaveSpan + (int)lane * VL + j * 64 * VL + e;
+              if (slot < (u32)kSoloList) L.u.fin.ent[slot] = ((u64)k << 32) | (u32)id;
+            }
+          }
+        };
+        if (total <= (u32)kSoloCBuf) {
+          // lanes take any of the wave's segments: LDS atomics
+          if (up && lane_id() < (u32)J) L.seg[sg0 + (int)lane_id()] = 0ull;
+          u64* cb = L.cbuf[wave_id()];
+          u32 pos = incl - cnt;
+#pragma unroll
+          for (int i = 0; i < E; ++i)
+            if ((set >> i) & 1u) cb[pos++] = ((u64)__float_as_uint(qv[i]) << 32) | (lane_id() << 4) | (u32)i;
+          // the wave's own LDS writes: complete before its lanes read each other's
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          auto add = [&](int j, u64 w) {
+            if (w) atomicAdd(&L.seg[sg0 + j], up ? w : (u64)0 - w);
+          };
+          auto tie = [&](int j) { atomicAdd(&L.segt[sg0 + j], 1u); };
+          for (u32 x = lane_id(); x < total; x += 64) {
+            const u64 en = cb[x];
+            const u32 i = (u32)en & 15u;
+            take(__uint_as_float((u32)(en >> 32)), (int)(i / VL), (int)(i % VL), ((u32)en >> 4) & 63u, add, tie);
+          }
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // read before the next chunk writes the buffer again
+        } else {
+          // in place: the wave's elements of one vector position j are one
+          // segment, summed in registers
+          auto tie = [&](int j) { atomicAdd(&L.segt[sg0 + j], 1u); };
+#pragma unroll
+          for (int j = 0; j < J; ++j) {
+            u64 sj = 0;
+            auto add = [&](int, u64 w) { sj += w; };
+#pragma unroll
+            for (int e = 0; e < VL; ++e)
+              if ((set >> (j * VL + e)) & 1u) take(qv[j * VL + e], j, e, lane_id(), add, tie);
+            const u64 sw = wave_sum64(sj);
+            if (lane_id() == 0) L.seg[sg0 + j] = up ? sw : L.seg[sg0 + j] - sw;
+          }
+        }
+        // the next chunk weighs the other side when this one took more than half
+        if (total > 32u * (u32)E) up = !up;
       });
     });
-    nzb = block_sum(nzb, L.s);
-    const u32 na = nz - nzb;  // tokens above the bracket with nonzero weight
+    const u32 na = nnan - block_sum(nab, L.s);  // tokens above the bracket
     if (!single) {
       const u32 n = uni(L.nlist);
       if (n > (u32)kSoloList || n == 0u) {  // the bound was exceeded: cannot happen
