@@ -1599,6 +1599,12 @@ __device__ __forceinline__ u32 mass_bin_d(float d, const MassBins& m) {
 __device__ __forceinline__ u32 mass_bin(float q, u32 k, float qs, u32 ks, const MassBins& m) {
   return mass_bin_d((k == ks) ? 0.0f : q - qs, m);
 }
+// mass_bin_d for the first round's bins (x0 = 0), the same bin: x = -d, and the
+// clamp to [0, kNB - 1] before the conversion (a dead token's NaN is not binned).
+__device__ __forceinline__ u32 mass_bin_first(float d, const MassBins& m) {
+  const float f = fminf(d * -m.s1, __builtin_fmaf(d, -m.s2, m.c2));
+  return (u32)__builtin_amdgcn_fmed3f(f, 0.0f, (float)(kNB - 1));
+}
 // x at the far edge of bin b
 __device__ __forceinline__ float bin_edge(const MassBins& m, u32 b) {
   const float e = (float)(b + 1);

@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
               const float d = q - qs;
               w = weight_finite(d, flmin, SH);
               if constexpr (M == 2) w = (q >= qk && w >= thr) ? w : 0ull;
-              if (p.topp && w) atomicAdd(&L.mh[mass_bin_d(d, br.mb0)], w);
+              if (p.topp && w) atomicAdd(&L.mh[mass_bin_first(d, br.mb0)], w);
             }
             sj += w;
             nz += w ? 1u : 0u;
