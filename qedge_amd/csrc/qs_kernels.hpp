@@ -127,6 +127,7 @@ struct Args {
 struct RowP {
   float T, rT, tp, mp, rep, rrep, pres, freq, u;
   int k, kind, hlen;
+  u32 dspan;  // qdiv's range of |z| bits for the fast division (0: none)
   bool t_one, topp, pen;
   const int* hist;
 };
@@ -163,7 +164,17 @@ __device__ __forceinline__ RowP row_params(const Args& a, int row) {
   p.kind = greedy ? kKindGreedy : (topk_on ? (p.k <= kTopkMax ? kKindTopK : kKindSingle) : kKindMass);
   p.t_one = __float_as_uint(p.T) == 0x3f800000u;  // T == 1
   p.rT = 1.0f / p.T;
+  // T in [2^-16, 2^16]: |z| in [2^-80, 2^80) keeps |z * rT| in [2^-100, 2^100)
+  p.dspan = __float_as_uint(p.T) - 0x37800000u <= 0x10000000u ? 0x50000000u : 0u;
   return p;
+}
+
+// The contract's q = z / T (one IEEE division) of the row: z itself for T = 1,
+// else the fast division (div_fast) where div_fast_ok holds by the ranges of z
+// and T alone, the division otherwise.
+__device__ __forceinline__ float qdiv(float z, const RowP& p) {
+  if (p.t_one) return z;
+  return (__float_as_uint(z) & 0x7fffffffu) - 0x17800000u < p.dspan ? div_fast(z, p.T, p.rT) : z / p.T;
 }
 
 // ---------------------------------------------------------------- LDS
@@ -381,7 +392,7 @@ __device__ __forceinline__ void chunk_qkeys(const Chunk<DT>& ch, const RowP& p, 
     for (int j = 0; j < Chunk<DT>::J; ++j)
 #pragma unroll
       for (int e = 0; e < Chunk<DT>::VL; ++e) {
-        const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+        const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p);
         kq[j * Chunk<DT>::VL + e] = skey(q);  // 0 past V (NaN padding)
       }
   });
@@ -703,7 +714,7 @@ __device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, 
   u32 kmax = 0, kmin = 0xffffffffu;
   u64 gbest = 0;
   row_pass<DT>(a, p, row, L, [&](float z, int id) {
-    const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));
+    const u32 k = skey(qdiv(z, p));
     kmax = max(kmax, k);
     if (k) kmin = min(kmin, k);
     const u64 pk = ((u64)gkey(z) << 32) | (0xffffffffu - (u32)id);
@@ -718,7 +729,7 @@ __device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, 
   }
   const float qs = f_of_key(kmax);
   auto key_w = [&](float z, u32& k) -> u64 {
-    const float q = qdiv(z, p.T, p.rT, p.t_one);
+    const float q = qdiv(z, p);
     k = skey(q);
     const u64 w = weight_of(q, k, qs, kmax, SH);
     return w >= thr ? w : 0ull;
@@ -731,7 +742,7 @@ __device__ __forceinline__ void resolve_single(const Args& a, int row, u32 why, 
     for (;;) {
       sel_clear(L);
       lds_sync();
-      row_pass<DT>(a, p, row, L, [&](float z, int) { sel_add(q, L, skey(qdiv(z, p.T, p.rT, p.t_one)), 0); });
+      row_pass<DT>(a, p, row, L, [&](float z, int) { sel_add(q, L, skey(qdiv(z, p)), 0); });
       lds_sync();
       if (sel_step(q, L)) break;
     }
@@ -1401,7 +1412,7 @@ __device__ __forceinline__ int finish_sorted(const Args& a, const RowP& p, int r
     } else {
       kk = readlane(key, p.k - 1);
       // completeness: every token left out has a key of q below kappa_k
-      if (below_max != 0u && skey(qdiv(f_of_key(below_max), p.T, p.rT, p.t_one)) >= kk) res = 0;
+      if (below_max != 0u && skey(qdiv(f_of_key(below_max), p)) >= kk) res = 0;
       if (n > 64u && readlane(key, 63) == kk) res = -1;  // ties at kappa_k may go on past the 64
     }
     if (res == 1) {
@@ -1481,7 +1492,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
     kk = q.kappa;
     nk = q.cnt_above + q.cnt_at;
     // completeness: every token left out has a key of q below kappa_k
-    if (below_max != 0u && skey(qdiv(f_of_key(below_max), p.T, p.rT, p.t_one)) >= kk) return false;
+    if (below_max != 0u && skey(qdiv(f_of_key(below_max), p)) >= kk) return false;
   }
   QS_TR(10);
   if (nk <= 64u) return finish_small_k(a, p, row, L, h, kk, nk, kmax, thr, wpk);
@@ -1765,8 +1776,8 @@ struct TkOut {
 // above which every token of the chunk is in its region.
 __device__ __forceinline__ void topk_slot(const Args& a, const RowP& p, const int row, const int c, const TkOut& t) {
   Slot* sl = row_slots(a, row);
-  const u32 qmax = t.zmax ? skey(qdiv(f_of_key(t.zmax), p.T, p.rT, p.t_one)) : 0u;
-  const u32 qlow = skey(qdiv(f_of_key(t.tau32), p.T, p.rT, p.t_one));
+  const u32 qmax = t.zmax ? skey(qdiv(f_of_key(t.zmax), p)) : 0u;
+  const u32 qlow = skey(qdiv(f_of_key(t.tau32), p));
   stc(&sl[c].a, ((u64)t.below << 32) | t.n);
   stc(&sl[c].d, ((u64)qmax << 32) | qlow);
 }
@@ -1793,7 +1804,7 @@ __device__ __forceinline__ u32 topk_last(const Args& a, const RowP& p, const int
     v[2] = ~(u32)d;         // the complement of the key of the chunk's threshold
     return (u32)x;
   };
-  auto qkey = [&](u32 zkey) -> u32 { return skey(qdiv(f_of_key(zkey), p.T, p.rT, p.t_one)); };
+  auto qkey = [&](u32 zkey) -> u32 { return skey(qdiv(f_of_key(zkey), p)); };
   u32 tot;
   if (zk)
     tot = gather_lds(a, row_data(a, row), R, cnt_of, L, mx,
@@ -1907,7 +1918,7 @@ __device__ __forceinline__ TkOut topk_row(const Args& a, const RowP& p, const in
       for (int e = 0; e < VL; ++e) {
         const u32 kx = kz[j * VL + e];
         if (kx >= tau) {
-          const float q = qdiv(f_of_key(kx), p.T, p.rT, p.t_one);
+          const float q = qdiv(f_of_key(kx), p);
           stc(&reg[pos], ((u64)skey(q) << 32) | (u32)ch.id(j, e));
           ++pos;
         }
@@ -2759,7 +2770,7 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
   if (threadIdx.x < 64) {
     const bool topp = p.topp;
     const long long id = seg_find<DT>(a, p, row, L, owner * nsg + (int)sloc, tin2, [&](float z, int i) -> u64 {
-      const float q = qdiv(z, p.T, p.rT, p.t_one);
+      const float q = qdiv(z, p);
       const u32 k = skey(q);
       u64 w = weight_of(q, k, qs, kstar, SH);
       w = w >= thr ? w : 0ull;

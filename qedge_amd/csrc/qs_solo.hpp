@@ -241,8 +241,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     block_max2(kx, kn, L.s);
     nnan = block_sum(nnan, L.s);
     if (nnan) {
-      kmax = skey(qdiv(f_of_key(kx), p.T, p.rT, p.t_one));
-      kmin = skey(qdiv(f_of_key(~kn), p.T, p.rT, p.t_one));
+      kmax = skey(qdiv(f_of_key(kx), p));
+      kmin = skey(qdiv(f_of_key(~kn), p));
     }
     gbest = 0xffffffffu;  // every z NaN: the first id
   } else {
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
           for (int e = 0; e < VL; ++e) {
             const float z = elem_zt<PEN>(ch, p, pw, j, e);
-            const u32 k = skey(qdiv(z, p.T, p.rT, p.t_one));  // 0 past V (NaN padding)
+            const u32 k = skey(qdiv(z, p));  // 0 past V (NaN padding)
             kmax = max(kmax, k);
             kmin = k ? min(kmin, k) : kmin;
             nnan += k ? 1u : 0u;
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
           for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int e = 0; e < VL; ++e) {
-              const u32 k = skey(qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one));
+              const u32 k = skey(qdiv(elem_zt<PEN>(ch, p, pw, j, e), p));
               if (k >= lo && k <= hi && k) atomicAdd(&L.hc[(hi - k) >> sh], 1u);
             }
         });
@@ -370,12 +370,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
             const float z = elem_zt<PEN>(ch, p, pw, j, e);
             u64 w;
             if constexpr (M == 0) {
-              const float q = qdiv(z, p.T, p.rT, p.t_one);
+              const float q = qdiv(z, p);
               const u32 k = skey(q);
               w = wunpack(wpk(q, k));
               if (p.topp && w) atomicAdd(&L.mh[mass_bin(q, k, qs, kmax, br.mb0)], w);
             } else {
-              const float q = M == 1 ? z : qdiv(z, p.T, p.rT, p.t_one);
+              const float q = M == 1 ? z : qdiv(z, p);
               const float d = q - qs;
               w = weight_finite(d, flmin, SH);
               if constexpr (M == 2) w = (q >= qk && w >= thr) ? w : 0ull;
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
             for (int j = 0; j < J; ++j)
 #pragma unroll
               for (int e = 0; e < VL; ++e) {
-                const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+                const float q = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p);
                 const u32 k = skey(q);
                 if (k && k >= br.lo && k <= br.hi) {
                   const u64 w = wunpack(wpk(q, k));
@@ -553,7 +553,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
             for (int e = 0; e < VL; ++e) {
               const int i = j * VL + e;
-              qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+              qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p);
               set |= qv[i] >= qlo ? 1u << i : 0u;
               nv += qv[i] == qv[i] ? 1u : 0u;
             }
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 #pragma unroll
             for (int e = 0; e < VL; ++e) {
               const int i = j * VL + e;
-              qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p.T, p.rT, p.t_one);
+              qv[i] = qdiv(elem_zt<PEN>(ch, p, pw, j, e), p);
               set |= qv[i] <= qhi ? 1u << i : 0u;
             }
           nab += (u32)__popc(set);
@@ -719,7 +719,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         if (p.pen) pen_build(p, (int)sg / (kWaves * J), L);
         if (threadIdx.x < 64) {
           const long long id = seg_find<DT>(a, p, row, L, (int)sg, (u64)within, [&](float z, int) -> u64 {
-            const float q = qdiv(z, p.T, p.rT, p.t_one);
+            const float q = qdiv(z, p);
             const u32 k = skey(q);
             return (k == klo && wpk(q, k)) ? 1ull : 0ull;
           });
@@ -776,7 +776,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
   if (threadIdx.x < 64) {
     const bool topp = p.topp;
     const long long id = seg_find<DT>(a, p, row, L, (int)sg, tin, [&](float z, int i) -> u64 {
-      const float q = qdiv(z, p.T, p.rT, p.t_one);
+      const float q = qdiv(z, p);
       const u32 k = skey(q);
       const u64 w = wunpack(wpk(q, k));
       if (!topp) return w;

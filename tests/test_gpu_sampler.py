@@ -493,3 +493,23 @@ def test_graph_replays_with_row_order(gpu):
             np.testing.assert_array_equal(outs[s].cpu().numpy(), eager[s])
         steps()  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_temperatures_outside_the_fast_division_range(gpu, dtype):
+    """Rows whose T lies outside [2^-16, 2^16] take the IEEE division for every
+    logit; rows inside it take the fast one for logits in [2^-80, 2^80) and the
+    division for zeros, tiny and huge logits."""
+    rng = np.random.default_rng(31)
+    V = 8192 * 3 + 77
+    x = (rng.standard_normal((6, V)) * 2).astype(np.float32)
+    x[0, :50] = 0.0
+    x[1, 10:20] = 1e-30  # below 2^-80
+    x[2, 30:40] = 3e25   # above 2^80
+    T = np.array([1.2e-5, 7e4, 0.7, 2.0 ** -16, 2.0 ** 16, 1e-4], np.float32)
+    if dtype == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        x = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    P = np.array([0.9, 0.8, 0.95, 0.7, 1.0, 0.9], np.float32)
+    K = np.array([0, 40, 0, 0, 0, 300], np.int32)
+    _check(x, dtype, gpu, T, P, K, u=rng.random(6).astype(np.float32))
