@@ -2286,23 +2286,49 @@ __device__ __forceinline__ u32 mass_row(const Args& a, const RowP& p, const int 
     u32 nz = 0, inb = 0;
 #pragma unroll
     for (int i = 0; i < E / 4; ++i) bq[i] = 0u;
+    // A finite q* without min_p (the common row): the weight straight from
+    // d = q - q* (weight_finite's clamp, no keys, no unpacking), packed for the
+    // later rounds; the keyed form otherwise.
+    const float flmin = -(float)(SH + 40);
+    auto weigh = [&](auto plain) {
+      constexpr bool PLAIN = decltype(plain)::value;
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const u32 k = L.u.kq[i * kThreads + threadIdx.x];
-      const float q = f_of_key(k);
-      u32 x = wpack_of(q, k, qs, kstar, SH);
-      x = x >= pthr ? x : 0u;
-      const u64 w = wunpack(x);
-      wp[i] = x;
-      Sc += x ? w : 0ull;
-      nz += x ? 1u : 0u;
-      inb |= (x ? 1u : 0u) << i;
-      if (p.topp && x) {
-        const u32 bi = mass_bin(q, k, qs, kstar, mb);
-        bq[i / 4] |= bi << (8 * (i % 4));
-        atomicAdd(&L.mh[bi], w);
+      for (int i = 0; i < E; ++i) {
+        const u32 k = L.u.kq[i * kThreads + threadIdx.x];
+        const float q = f_of_key(k);
+        u32 x;
+        u64 w;
+        if constexpr (PLAIN) {
+          const float d = q - qs;
+          const float y = d * kL2E;
+          const float fl = __builtin_floorf(y);
+          const float f = y - fl;
+          float pe = exp2_poly(f);
+          pe = __builtin_amdgcn_fmed3f(pe, 1.0f, __uint_as_float(0x3fffffffu));
+          const u32 m = 0x800000u | (__float_as_uint(pe) & 0x7fffffu);
+          const int sx = (int)fmaxf(fl, flmin) + SH;
+          w = ((u64)m << max(sx, 0)) >> max(-sx, 0);
+          x = sx > -24 ? ((u32)(sx + 64) << 24) | m : 0u;  // wpack_of's form: w != 0 exactly then
+        } else {
+          x = wpack_of(q, k, qs, kstar, SH);
+          x = x >= pthr ? x : 0u;
+          w = wunpack(x);
+        }
+        wp[i] = x;
+        Sc += w;
+        nz += x ? 1u : 0u;
+        inb |= (x ? 1u : 0u) << i;
+        if (p.topp && x) {
+          const u32 bi = PLAIN ? mass_bin_first(q - qs, mb) : mass_bin(q, k, qs, kstar, mb);
+          bq[i / 4] |= bi << (8 * (i % 4));
+          atomicAdd(&L.mh[bi], w);
+        }
       }
-    }
+    };
+    if (qs - qs == 0.0f && pthr == 0u)
+      weigh(Tag<true>{});
+    else
+      weigh(Tag<false>{});
     QS_TR(5);
     if (!p.topp) {  // every weight is kept: the segments' masses
       u64* sg = seg_base(a, row) + (size_t)c * kSegMax;
