@@ -1649,7 +1649,7 @@ __device__ __forceinline__ MassBins mass_bins_split(const MassBins& m, u32 b) {
 // The chunk's history table must be built.
 template <int DT, typename LT, typename VF>
 __device__ __forceinline__ long long seg_find(const Args& a, const RowP& p, int row, const LT& L, int s, u64 t,
-                                              VF&& val) {
+                                              VF&& val, u64* seg_total = nullptr) {
   constexpr int VL = Chunk<DT>::VL, J = Chunk<DT>::J;
   const int c = s / (kWaves * J), w = (s / J) % kWaves, j = s % J;
   const int l = lane_id();
@@ -1689,6 +1689,7 @@ __device__ __forceinline__ long long seg_find(const Args& a, const RowP& p, int 
     tot += v[e];
   }
   const u64 inc = wave_incl_scan64(tot);
+  if (seg_total) *seg_total = ((u64)readlane((u32)(inc >> 32), 63) << 32) | readlane((u32)inc, 63);
   u64 m = inc - tot;
   long long pick = -1;
 #pragma unroll

@@ -9,7 +9,7 @@
 //   rounds  while the bin holding the top-p boundary is too large: one more
 //           pass histograms the bin's tokens by key (256 bins, counts and mass)
 //   pass 3  the bracket's tokens listed (key, id) in LDS, the mass above it per
-//           segment (a segment is one wave's vector span of one chunk: 64 * VL ids)
+//           segment (a segment is one wave's share of one chunk: kWaveSpan ids)
 //   final   the exact boundary among the listed tokens, the segment holding the
 //           draw, and the token inside it from one wave's re-read of the segment.
 #pragma once
@@ -19,7 +19,7 @@
 namespace qs {
 
 constexpr int kSoloList = 2048;   // bracket tokens listed in LDS
-constexpr int kSoloSegs = 1024;   // segments per row (G * kWaves * J)
+constexpr int kSoloSegs = 1024;   // segments per row (G * kWaves)
 constexpr int kSoloRounds = 6;    // bracket rounds: the first in x = q* - q, then in key space
 constexpr int kSoloHist = 4096;   // history ids copied to LDS (the rest are read from memory)
 constexpr int kSoloCBuf = 128;    // pass 3: tokens at or below the bracket per wave and chunk, compacted
@@ -55,10 +55,21 @@ __device__ __forceinline__ int hist_id(const RowP& p, const SoloLds& L, int i) {
   return i < kSoloHist ? L.hist[i] : gld(p.hist + i);
 }
 
-// Segment of a token id: one wave's vector span (64 * VL ids) of a chunk.
-template <int DT>
-__device__ __forceinline__ int seg_of(int id) {
-  return id / (64 * Chunk<DT>::VL);
+// Segment of a token id: one wave's share (kWaveSpan ids) of a chunk.
+__device__ __forceinline__ int solo_seg_of(int id) { return id / kWaveSpan; }
+// seg_find over segment s (its J vector spans in id order): the id where the
+// running total of val passes t, or -1.
+template <int DT, typename VF>
+__device__ __forceinline__ long long solo_seg_find(const Args& a, const RowP& p, int row, const SoloLds& L, int s,
+                                                   u64 t, VF&& val) {
+  constexpr int J = Chunk<DT>::J;
+  for (int j = 0; j < J; ++j) {
+    u64 tot;
+    const long long id = seg_find<DT>(a, p, row, L, s * J + j, t, val, &tot);
+    if (id >= 0) return id;
+    t -= tot;  // the span's total is at most t
+  }
+  return -1;
 }
 
 // Loads of chunk c for the streaming passes with 16-byte vectors (Args::vec_ok
@@ -336,7 +347,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     const u32 x = (k >= kk && k) ? wpack_of(q, k, qs, kmax, SH) : 0u;
     return x >= pthr ? x : 0u;
   };
-  const int nseg = a.G * kWaves * J;
+  const int nseg = a.G * kWaves;
   QS_TRS(2);
   // ---- pass 2: weights, S, per-segment masses, the first bracket histogram
   Bracket br;
@@ -362,9 +373,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       if constexpr (PEN) chunk_counts(L, ch, c, pw);
       auto body = [&](auto mode) {
         constexpr int M = decltype(mode)::value;
+        u64 sj = 0;  // the segment's mass
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-          u64 sj = 0;
 #pragma unroll
           for (int e = 0; e < VL; ++e) {
             const float z = elem_zt<PEN>(ch, p, pw, j, e);
@@ -384,10 +395,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
             sj += w;
             nz += w ? 1u : 0u;
           }
-          const u64 sw = wave_sum64(sj);
-          if (lane_id() == 0) L.seg[(c * kWaves + wave_id()) * J + j] = sw;
-          S += lane_id() == 0 ? sw : 0ull;
         }
+        const u64 sw = wave_sum64(sj);
+        if (lane_id() == 0) L.seg[c * kWaves + wave_id()] = sw;
+        S += lane_id() == 0 ? sw : 0ull;
       };
       if (wmode == 1)
         body(ITag<1>{});
@@ -572,19 +583,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
         const u32 cnt = (u32)__popc(set);
         const u32 incl = wave_incl_scan(cnt);
         const u32 total = readlane(incl, 63);
-        const int sg0 = (c * kWaves + wave_id()) * J;
+        const int sg = c * kWaves + wave_id();
         // one weighed token: its weight to (above) or off (at or below) its
         // segment's mass, and a bracket token listed (or counted, for a bracket
-        // of one key); add(j, w) and tie(j) take the segment's share
+        // of one key); add(w) and tie() take the segment's share
         auto take = [&](float q, int j, int e, u32 lane, auto&& add, auto&& tie) {
           const u32 k = skey(q);
           const int side = bracket_side(br, k);
           const u64 w = wunpack(wpk(q, k));
-          if (up ? side == 0 : true) add(j, w);
+          if (up ? side == 0 : true) add(w);
           if (up && side == 1) ++nab;
           if (side == 1 && w) {
             if (single) {
-              tie(j);
+              tie();
             } else {
               const u32 slot = atomicAdd(&L.nlist, 1u);
               const int id = c * kCH + wave_id() * kWaveSpan + (int)lane * VL + j * 64 * VL + e;
@@ -593,8 +604,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
           }
         };
         if (total <= (u32)kSoloCBuf) {
-          // lanes take any of the wave's segments: LDS atomics
-          if (up && lane_id() < (u32)J) L.seg[sg0 + (int)lane_id()] = 0ull;
+          // lanes take tokens of any of the wave's elements: LDS atomics
+          if (up && lane_id() == 0) L.seg[sg] = 0ull;
           u64* cb = L.cbuf[wave_id()];
           u32 pos = incl - cnt;
 #pragma unroll
@@ -602,10 +613,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
             if ((set >> i) & 1u) cb[pos++] = ((u64)__float_as_uint(qv[i]) << 32) | (lane_id() << 4) | (u32)i;
           // the wave's own LDS writes: complete before its lanes read each other's
           __builtin_amdgcn_s_waitcnt(0xC07F);
-          auto add = [&](int j, u64 w) {
-            if (w) atomicAdd(&L.seg[sg0 + j], up ? w : (u64)0 - w);
+          auto add = [&](u64 w) {
+            if (w) atomicAdd(&L.seg[sg], up ? w : (u64)0 - w);
           };
-          auto tie = [&](int j) { atomicAdd(&L.segt[sg0 + j], 1u); };
+          auto tie = [&]() { atomicAdd(&L.segt[sg], 1u); };
           for (u32 x = lane_id(); x < total; x += 64) {
             const u64 en = cb[x];
             const u32 i = (u32)en & 15u;
@@ -613,19 +624,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);  // read before the next chunk writes the buffer again
         } else {
-          // in place: the wave's elements of one vector position j are one
-          // segment, summed in registers
-          auto tie = [&](int j) { atomicAdd(&L.segt[sg0 + j], 1u); };
+          // in place: the segment's share summed in registers
+          auto tie = [&]() { atomicAdd(&L.segt[sg], 1u); };
+          u64 sj = 0;
+          auto add = [&](u64 w) { sj += w; };
 #pragma unroll
-          for (int j = 0; j < J; ++j) {
-            u64 sj = 0;
-            auto add = [&](int, u64 w) { sj += w; };
+          for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int e = 0; e < VL; ++e)
               if ((set >> (j * VL + e)) & 1u) take(qv[j * VL + e], j, e, lane_id(), add, tie);
-            const u64 sw = wave_sum64(sj);
-            if (lane_id() == 0) L.seg[sg0 + j] = up ? sw : L.seg[sg0 + j] - sw;
-          }
+          const u64 sw = wave_sum64(sj);
+          if (lane_id() == 0) L.seg[sg] = up ? sw : L.seg[sg] - sw;
         }
         // the next chunk weighs the other side when this one took more than half
         if (total > 32u * (u32)E) up = !up;
@@ -679,7 +688,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
       for (int i = 0; i < kFPer; ++i) {
         if ((u32)i < h.per && wq[i]) {
           const u32 k = (u32)(h.e[i] >> 32), id = (u32)h.e[i];
-          if (k > klo || (k == klo && id <= idlo)) atomicAdd(&L.seg[seg_of<DT>((int)id)], wunpack(wq[i]));
+          if (k > klo || (k == klo && id <= idlo)) atomicAdd(&L.seg[solo_seg_of((int)id)], wunpack(wq[i]));
         }
       }
       lds_sync();
@@ -716,9 +725,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
           write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStList, kmax, 0u, 0u, 0u);
           return;
         }
-        if (p.pen) pen_build(p, (int)sg / (kWaves * J), L);
+        if (p.pen) pen_build(p, (int)sg / kWaves, L);
         if (threadIdx.x < 64) {
-          const long long id = seg_find<DT>(a, p, row, L, (int)sg, (u64)within, [&](float z, int) -> u64 {
+          const long long id = solo_seg_find<DT>(a, p, row, L, (int)sg, (u64)within, [&](float z, int) -> u64 {
             const float q = qdiv(z, p);
             const u32 k = skey(q);
             return (k == klo && wpk(q, k)) ? 1ull : 0ull;
@@ -772,10 +781,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
     write_result(a, row, p, -1ll, 0, thr, kPathSolo, kStIncomplete, kmax, 0u, 0u, 0u);
     return;
   }
-  if (p.pen) pen_build(p, (int)sg / (kWaves * J), L);
+  if (p.pen) pen_build(p, (int)sg / kWaves, L);
   if (threadIdx.x < 64) {
     const bool topp = p.topp;
-    const long long id = seg_find<DT>(a, p, row, L, (int)sg, tin, [&](float z, int i) -> u64 {
+    const long long id = solo_seg_find<DT>(a, p, row, L, (int)sg, tin, [&](float z, int i) -> u64 {
       const float q = qdiv(z, p);
       const u32 k = skey(q);
       const u64 w = wunpack(wpk(q, k));

@@ -189,8 +189,7 @@ int qs_sample(const void* logits, int64_t row_stride, int logits_dtype, int B, i
   a.trace = (u64*)g_trace;
 #endif
   const dim3 grid(L.G, B), block(kThreads);
-  const int J = logits_dtype == QS_DTYPE_F32 ? 4 : 2;  // 16-byte vectors per thread and chunk
-  const bool solo = (flags & QS_FLAG_SOLO) && L.G * kWaves * J <= kSoloSegs;
+  const bool solo = (flags & QS_FLAG_SOLO) && L.G * kWaves <= kSoloSegs;  // one segment per wave and chunk
   if (solo) {
     // 16-byte vector loads need aligned rows and at least one whole vector
     const bool vec = a.vec_ok && a.V >= (logits_dtype == QS_DTYPE_F32 ? 4 : 8);

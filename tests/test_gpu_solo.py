@@ -126,3 +126,16 @@ def test_penalties_and_long_histories(gpu):
     pres = np.array([0.5, 0.0, 0.3, 0.2, 0.0, 1.0], np.float32)
     freq = np.array([0.3, 0.1, 0.0, 0.05, 0.5, 0.0], np.float32)
     _solo(X, "bf16", gpu, T, P, None, rep, pres, freq, hist, rng.random(B).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_long_rows(gpu, dtype):
+    """V = 600001: 74 chunks, 592 segments per row."""
+    V = 600001
+    rng = np.random.default_rng(41)
+    X = (rng.standard_normal((3, V)) * np.array([[0.05], [1.5], [3.0]])).astype(np.float32)
+    if dtype == "bf16":
+        X = _bf16(X)
+    T = np.array([1.0, 0.7, 1.1], np.float32)
+    P = np.array([0.95, 0.9, 0.6], np.float32)
+    _solo(X, dtype, gpu, T, P, u=rng.random(3).astype(np.float32))
