@@ -52,9 +52,9 @@ extern "C" {
 #define QS_FLAG_SOLO 8u       /* resolve every row by one workgroup streaming it (no
                                  workgroup cooperation): faster for batches of hundreds
                                  of rows with top-k off; rows with top-k on take extra
-                                 passes.  Ignored where a row spans more than 1024
-                                 wave segments (V > 262144 fp32, V > 524288 bf16).
-                                 Results are identical. */
+                                 passes.  Ignored where a row spans more than 128
+                                 chunks of 8192 logits (V > 1048576).  Results are
+                                 identical. */
 
 #define QS_TOPK_FAST_MAX 1024 /* top_k up to this value is resolved from
                                  per-chunk candidates in one pass; larger
