@@ -1542,12 +1542,11 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   }
   u32 ttot;
   u64 mtot;
-  block_excl2(tc, m, L.s, &ttot, &mtot);
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0) {  // ordered before the stores below by block_excl2's barriers
     L.s.r[11] = 0xffffffffu;
     L.s.r[12] = 0xffffffffu;
   }
-  lds_sync();
+  block_excl2(tc, m, L.s, &ttot, &mtot);
 #pragma unroll
   for (int i = 0; i < kFPer; ++i) {
     if ((u32)i < h.per) {
