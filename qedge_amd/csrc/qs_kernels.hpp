@@ -1011,8 +1011,11 @@ struct SelRes {
 };
 // With frac >= 0 (by mass) the target is floor(frac * total), the total being
 // the range's mass, found in the first round; the totals are returned.  The
-// histogram has two buffers: a round clears the next one's.
-template <bool BY_MASS, typename LT>
+// histogram has two buffers: a round clears the next one's.  Without TAIL
+// the select returns with no closing barrier: the caller must not write the
+// scratch fields the result is read from (r[4..10], r64[4..7]) before its next
+// barrier.
+template <bool BY_MASS, bool TAIL = true, typename LT>
 __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& h, const u32 (&wq)[kFPer], u32 lo,
                                               u32 hi, u64 target, float frac = -1.0f) {
   (void)a;
@@ -1116,7 +1119,7 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
       r.cnt_at = cnt_b;
       r.mass_at = mass_b;
       r.ok = true;
-      lds_sync();
+      if (TAIL) lds_sync();
       return r;
     }
     hi = nhi;
@@ -1177,7 +1180,7 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
       r.mass_above += uni64(L.s.r64[6]);
       r.mass_at = uni64(L.s.r64[7]);
       r.ok = kx != 0xffffffffu;
-      lds_sync();
+      if (TAIL) lds_sync();
       return r;
     }
   }
@@ -1487,12 +1490,16 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
     kk = 1u;
     nk = n;
   } else {
-    const SelRes q = held_select<false>(a, L, h, wq, max(klow, 1u), kmax, (u64)p.k);
-    if (!q.ok) return false;
+    // no closing barrier: what follows writes none of the scratch fields the
+    // select's result is read from before its own first barrier
+    const SelRes q = held_select<false, false>(a, L, h, wq, max(klow, 1u), kmax, (u64)p.k);
     kk = q.kappa;
     nk = q.cnt_above + q.cnt_at;
     // completeness: every token left out has a key of q below kappa_k
-    if (below_max != 0u && skey(qdiv(f_of_key(below_max), p)) >= kk) return false;
+    if (!q.ok || (below_max != 0u && skey(qdiv(f_of_key(below_max), p)) >= kk)) {
+      lds_sync();  // the exact path reuses the scratch fields just read
+      return false;
+    }
   }
   QS_TR(10);
   if (nk <= 64u) return finish_small_k(a, p, row, L, h, kk, nk, kmax, thr, wpk);
@@ -1514,10 +1521,13 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   u64 W = S, wt = 0;
   QS_TR(11);
   if (p.topp) {
-    const SelRes q = held_select<true>(a, L, h, wq, kk, kmax, 0ull, p.tp);
+    const SelRes q = held_select<true, false>(a, L, h, wq, kk, kmax, 0ull, p.tp);
     S = q.total_mass;
     const u64 Tp = mul_frac(S, p.tp);
-    if (!q.ok) return false;
+    if (!q.ok) {
+      lds_sync();  // the exact path reuses the scratch fields just read
+      return false;
+    }
     klo = q.kappa;
     wt = wf(klo);  // every token at kappa_p has this weight
     const u64 jj = div_small(Tp - q.mass_above, wt) + 1ull;
