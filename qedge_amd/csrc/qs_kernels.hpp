@@ -1008,16 +1008,18 @@ struct SelRes {
   bool ok;
   u32 total_cnt;   // the first round's totals over the range
   u64 total_mass;
+  int clean;       // the histogram buffer (0 or 1) left cleared
 };
 // With frac >= 0 (by mass) the target is floor(frac * total), the total being
 // the range's mass, found in the first round; the totals are returned.  The
 // histogram has two buffers: a round clears the next one's.  Without TAIL
 // the select returns with no closing barrier: the caller must not write the
 // scratch fields the result is read from (r[4..10], r64[4..7]) before its next
-// barrier.
+// barrier.  With clean0 >= 0 the histogram buffer clean0 is known to be cleared
+// (a previous select's result) and the select starts on it without clearing.
 template <bool BY_MASS, bool TAIL = true, typename LT>
 __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& h, const u32 (&wq)[kFPer], u32 lo,
-                                              u32 hi, u64 target, float frac = -1.0f) {
+                                              u32 hi, u64 target, float frac = -1.0f, int clean0 = -1) {
   (void)a;
   SelRes r;
   r.kappa = r.cnt_above = r.cnt_at = 0u;
@@ -1025,15 +1027,20 @@ __device__ __forceinline__ SelRes held_select(const Args& a, LT& L, const Held& 
   r.ok = false;
   r.total_cnt = 0u;
   r.total_mass = 0ull;
-  for (int b = threadIdx.x; b < kNB; b += kThreads) {
-    L.sel.hc[b] = 0u;
-    L.sel.hm[b] = 0ull;
+  const int p0 = clean0 >= 0 ? clean0 : 0;
+  if (clean0 < 0) {
+    for (int b = threadIdx.x; b < kNB; b += kThreads) {
+      L.sel.hc[b] = 0u;
+      L.sel.hm[b] = 0ull;
+    }
+    lds_sync();
   }
-  lds_sync();
+  r.clean = p0;
   for (int round = 0; round < 6; ++round) {
     const int bl = bitlen(hi - lo);
     const int sh = bl > 8 ? bl - 8 : 0;
-    const int cur = (round & 1) * kNB, nxt = kNB - cur;
+    const int cur = ((round + p0) & 1) * kNB, nxt = kNB - cur;
+    r.clean = ((round + p0) & 1) ^ 1;  // nxt, cleared below
     if (round < 4) QS_TRA(15 + 3 * round);
 #pragma unroll
     for (int i = 0; i < kFPer; ++i) {
@@ -1485,6 +1492,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   QS_TR(9);
   // kappa_k
   u32 kk, nk;  // nk: the size of K (tokens with key >= kk)
+  int clean = -1;  // a select histogram buffer known to be cleared
   if (n < (u32)p.k) {
     if (below_max != 0u) return false;  // tokens left out could belong to K
     kk = 1u;
@@ -1493,6 +1501,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
     // no closing barrier: what follows writes none of the scratch fields the
     // select's result is read from before its own first barrier
     const SelRes q = held_select<false, false>(a, L, h, wq, max(klow, 1u), kmax, (u64)p.k);
+    clean = q.clean;
     kk = q.kappa;
     nk = q.cnt_above + q.cnt_at;
     // completeness: every token left out has a key of q below kappa_k
@@ -1521,7 +1530,7 @@ __device__ __forceinline__ bool finish_topk(const Args& a, const RowP& p, int ro
   u64 W = S, wt = 0;
   QS_TR(11);
   if (p.topp) {
-    const SelRes q = held_select<true, false>(a, L, h, wq, kk, kmax, 0ull, p.tp);
+    const SelRes q = held_select<true, false>(a, L, h, wq, kk, kmax, 0ull, p.tp, clean);
     S = q.total_mass;
     const u64 Tp = mul_frac(S, p.tp);
     if (!q.ok) {
